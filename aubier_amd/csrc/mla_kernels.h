@@ -1,0 +1,50 @@
+// mla_kernels.h -- host-visible launch interface of the gfx950 kernels (internal to the library;
+// the public boundary is include/mla_m4.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mla {
+
+// Split-K decode / generic attention launch arguments (byte strides throughout).
+struct DecodeArgs {
+    const char * kc;        // cache base
+    int64_t kc_nb1;         // cache row stride
+    const float * q;        // Qcur
+    int64_t q_nb1, q_nb2;   // head, token strides
+    const float * mask;     // may be null
+    int64_t mask_nb1;       // token stride
+    float scale_log2;       // kq_scale * log2(e)
+    int n_kv;
+    int n_head;
+    int nt;
+    int n_split;
+    int n_tiles;            // ceil(n_kv / 64)
+    float * part;           // partial records (when dst == null)
+    float * dst;            // final output (single-split launches), contiguous [D_v, nt, H]
+};
+
+hipError_t launch_kqkv_decode_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
+bool decode_f16_supported(int dk, int dv);
+
+// Generic VALU path (f32 or f16 cache, any D_k <= 1024, D_v <= D_k): one workgroup per
+// (split, head, token).  round16 applies the f16 rounding of q and P (F16 cache semantics).
+hipError_t launch_kqkv_generic(int dk, int dv, int kc_is_f16, const DecodeArgs & a, hipStream_t stream);
+
+// Split-K merge: part [(4 + dv), n_split, nt, H] -> dst [dv, nt, H]
+hipError_t launch_merge(const float * part, int dv, int n_split, int nt, int n_head, float * dst,
+                        hipStream_t stream);
+
+// WKB: dst[t][h][c] = sum_d w[h][c][d] * q[t][h][d]
+struct WkbArgs {
+    const float * w;        // contiguous [d_n, D_v, H]
+    const float * q;        // q_nope
+    int64_t q_nb1, q_nb2;
+    float * dst;
+    int64_t d_nb1, d_nb2;
+    int d_n, d_v, n_head, nt;
+};
+hipError_t launch_wkb_f32(const WkbArgs & a, hipStream_t stream);
+
+}  // namespace mla

@@ -1,0 +1,301 @@
+// mla_m4_abi.cpp -- the C ABI of include/mla_m4.h: host-side contract checks, path selection and
+// launches.  Nothing here allocates, synchronises or reads device memory, so every entry point is
+// legal inside hipGraph capture (the reference's plain-launch contract,
+// patches/ggml-m4/m4-kqkv.cuh:3-7).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "../../include/mla_m4.h"
+#include "mla_kernels.h"
+
+namespace {
+
+constexpr int TILE_KEYS = 64;        // the decode kernels' tile (whole tiles per split)
+constexpr int DECODE_HEADS = 32;     // heads per MFMA decode workgroup
+constexpr int TARGET_WG = 256;       // one wave of workgroups over the 256 CUs
+
+bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+size_t elsize(int32_t type) {
+    switch (type) {
+        case MLA_M4_TYPE_F32: return 4;
+        case MLA_M4_TYPE_F16: return 2;
+        default: return 0;
+    }
+}
+
+bool is_contiguous(const mla_m4_tensor * t) {
+    const size_t es = elsize(t->type);
+    if (es == 0) return false;
+    size_t expect = es;
+    for (int i = 0; i < 4; ++i) {
+        if (t->ne[i] != 1 && t->nb[i] != expect) return false;
+        expect *= (size_t)t->ne[i];
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------- KQKV contract
+struct KqkvShape {
+    int64_t dk, dv, n_kv, n_head, nt;
+    int32_t kc_type;
+    bool has_mask;
+};
+
+int check_kqkv(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_tensor * mask,
+               const mla_m4_tensor * dst, KqkvShape * s) {
+    if (!kc || !q || !dst || !kc->data || !q->data || !dst->data) return MLA_M4_ERR_NULL;
+    if (kc->type != MLA_M4_TYPE_F16 && kc->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
+    if (q->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
+    const size_t es = elsize(kc->type);
+    // kcache ne [D_k, n_kv, 1, 1]
+    if (kc->ne[0] < 1 || kc->ne[1] < 1 || kc->ne[2] != 1 || kc->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (kc->nb[0] != es || kc->nb[1] < (size_t)kc->ne[0] * es || (kc->nb[1] & 15u) || !aligned16(kc->data))
+        return MLA_M4_ERR_STRIDE;
+    // q ne [D_k, H, nt, 1]
+    if (q->ne[0] != kc->ne[0] || q->ne[1] < 1 || q->ne[2] < 1 || q->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (q->nb[0] != 4 || (q->nb[1] & 15u) || (q->nb[2] & 15u) || !aligned16(q->data)) return MLA_M4_ERR_STRIDE;
+    if (q->nb[1] < (size_t)q->ne[0] * 4) return MLA_M4_ERR_STRIDE;
+    // dst ne [D_v, nt, H, 1] contiguous
+    const int64_t dv = dst->ne[0];
+    if (dv < 4 || (dv & 3) || dv > kc->ne[0]) return MLA_M4_ERR_SHAPE;
+    if (dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (!is_contiguous(dst) || !aligned16(dst->data)) return MLA_M4_ERR_STRIDE;
+    // mask ne [n_kv, >= nt, 1, 1] (optional)
+    const bool has_mask = mask && mask->data;
+    if (has_mask) {
+        if (mask->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
+        if (mask->ne[0] != kc->ne[1] || mask->ne[1] < q->ne[2] || mask->ne[2] != 1 || mask->ne[3] != 1)
+            return MLA_M4_ERR_SHAPE;
+        if (mask->nb[0] != 4 || mask->nb[1] < (size_t)mask->ne[0] * 4) return MLA_M4_ERR_STRIDE;
+    }
+    if (kc->ne[1] > INT32_MAX || q->ne[1] > 65535 || q->ne[2] > 65535) return MLA_M4_ERR_UNSUPPORTED;
+    if (kc->ne[0] > 1024 || dv > 1024) return MLA_M4_ERR_UNSUPPORTED;
+    s->dk = kc->ne[0];
+    s->dv = dv;
+    s->n_kv = kc->ne[1];
+    s->n_head = q->ne[1];
+    s->nt = q->ne[2];
+    s->kc_type = kc->type;
+    s->has_mask = has_mask;
+    return MLA_M4_OK;
+}
+
+bool use_mfma(const KqkvShape & s) {
+    return s.kc_type == MLA_M4_TYPE_F16 && mla::decode_f16_supported((int)s.dk, (int)s.dv);
+}
+
+int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
+
+int default_splits(const KqkvShape & s) {
+    const int64_t tiles = n_tiles_of(s.n_kv);
+    int64_t groups;   // workgroups per split
+    if (use_mfma(s)) groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) * s.nt;
+    else groups = s.n_head * s.nt;
+    int64_t sp = (TARGET_WG + groups - 1) / groups;
+    if (sp > tiles) sp = tiles;
+    if (sp > MLA_M4_MAX_SPLITS) sp = MLA_M4_MAX_SPLITS;
+    if (sp < 1) sp = 1;
+    return (int)sp;
+}
+
+size_t part_bytes(const KqkvShape & s, int n_split) {
+    return (size_t)s.n_head * (size_t)s.nt * (size_t)n_split * (size_t)(MLA_M4_PART_HDR + s.dv) * sizeof(float);
+}
+
+mla::DecodeArgs make_args(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_tensor * mask,
+                          float kq_scale, const KqkvShape & s, int n_split) {
+    mla::DecodeArgs a{};
+    a.kc = static_cast<const char *>(kc->data);
+    a.kc_nb1 = (int64_t)kc->nb[1];
+    a.q = static_cast<const float *>(q->data);
+    a.q_nb1 = (int64_t)q->nb[1];
+    a.q_nb2 = (int64_t)q->nb[2];
+    a.mask = s.has_mask ? static_cast<const float *>(mask->data) : nullptr;
+    a.mask_nb1 = s.has_mask ? (int64_t)mask->nb[1] : 0;
+    a.scale_log2 = kq_scale * 1.4426950408889634f;
+    a.n_kv = (int)s.n_kv;
+    a.n_head = (int)s.n_head;
+    a.nt = (int)s.nt;
+    a.n_split = n_split;
+    a.n_tiles = (int)n_tiles_of(s.n_kv);
+    a.part = nullptr;
+    a.dst = nullptr;
+    return a;
+}
+
+int launch_attn(const KqkvShape & s, const mla::DecodeArgs & a, hipStream_t stream) {
+    hipError_t e;
+    if (use_mfma(s)) e = mla::launch_kqkv_decode_f16((int)s.dk, (int)s.dv, a, stream);
+    else e = mla::launch_kqkv_generic((int)s.dk, (int)s.dv, s.kc_type == MLA_M4_TYPE_F16, a, stream);
+    return e == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
+// ---------------------------------------------------------------- merge contract
+int check_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst) {
+    if (!part || !dst || !part->data || !dst->data) return MLA_M4_ERR_NULL;
+    if (part->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
+    const int64_t dv = part->ne[0] - MLA_M4_PART_HDR;
+    if (dv < 4 || (dv & 3) || part->ne[1] < 1 || part->ne[1] > MLA_M4_MAX_SPLITS) return MLA_M4_ERR_SHAPE;
+    if (dst->ne[0] != dv || dst->ne[1] != part->ne[2] || dst->ne[2] != part->ne[3] || dst->ne[3] != 1)
+        return MLA_M4_ERR_SHAPE;
+    if (part->ne[2] > 65535 || part->ne[3] > 65535) return MLA_M4_ERR_UNSUPPORTED;
+    if (!is_contiguous(part) || !is_contiguous(dst) || !aligned16(part->data) || !aligned16(dst->data))
+        return MLA_M4_ERR_STRIDE;
+    return MLA_M4_OK;
+}
+
+// ---------------------------------------------------------------- WKB contract
+int check_wkb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst) {
+    if (!w || !x || !dst || !w->data || !x->data || !dst->data) return MLA_M4_ERR_NULL;
+    if (w->type != MLA_M4_TYPE_F32 || x->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32)
+        return MLA_M4_ERR_TYPE;
+    const int64_t dn = w->ne[0], dv = w->ne[1], nh = w->ne[2];
+    if (dn < 1 || dv < 1 || nh < 1 || w->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (x->ne[0] != dn || x->ne[1] != nh || x->ne[2] < 1 || x->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (dst->ne[0] != dv || dst->ne[1] != nh || dst->ne[2] != x->ne[2] || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (!is_contiguous(w) || !aligned16(w->data)) return MLA_M4_ERR_STRIDE;
+    if (x->nb[0] != 4 || (x->nb[1] & 15u) || (x->nb[2] & 15u) || !aligned16(x->data)) return MLA_M4_ERR_STRIDE;
+    if (dst->nb[0] != 4 || (dst->nb[1] & 3u) || (dst->nb[2] & 3u)) return MLA_M4_ERR_STRIDE;
+    if (dst->nb[1] < (size_t)dv * 4) return MLA_M4_ERR_STRIDE;
+    if (dn != 64 && dn != 128) return MLA_M4_ERR_UNSUPPORTED;
+    if (dv % 16 != 0 || nh * dv > INT32_MAX || x->ne[2] > INT32_MAX) return MLA_M4_ERR_UNSUPPORTED;
+    return MLA_M4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char * mla_m4_version(void) { return "mla-m4-gfx950 0.1"; }
+
+const char * mla_m4_status_str(int status) {
+    switch (status) {
+        case MLA_M4_OK: return "ok";
+        case MLA_M4_ERR_NULL: return "null tensor or data pointer";
+        case MLA_M4_ERR_TYPE: return "unsupported element type";
+        case MLA_M4_ERR_SHAPE: return "shape violates the op contract";
+        case MLA_M4_ERR_STRIDE: return "strides/alignment violate the op contract";
+        case MLA_M4_ERR_WORKSPACE: return "workspace missing or too small";
+        case MLA_M4_ERR_ARG: return "scalar argument out of range";
+        case MLA_M4_ERR_LAUNCH: return "HIP launch failed";
+        case MLA_M4_ERR_UNSUPPORTED: return "shape not implemented by these kernels";
+        default: return "unknown status";
+    }
+}
+
+int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope, const mla_m4_tensor * dst, void * stream) {
+    const int rc = check_wkb(w, q_nope, dst);
+    if (rc != MLA_M4_OK) return rc;
+    mla::WkbArgs a{};
+    a.w = static_cast<const float *>(w->data);
+    a.q = static_cast<const float *>(q_nope->data);
+    a.q_nb1 = (int64_t)q_nope->nb[1];
+    a.q_nb2 = (int64_t)q_nope->nb[2];
+    a.dst = static_cast<float *>(dst->data);
+    a.d_nb1 = (int64_t)dst->nb[1];
+    a.d_nb2 = (int64_t)dst->nb[2];
+    a.d_n = (int)w->ne[0];
+    a.d_v = (int)w->ne[1];
+    a.n_head = (int)w->ne[2];
+    a.nt = (int)q_nope->ne[2];
+    return mla::launch_wkb_f32(a, static_cast<hipStream_t>(stream)) == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
+size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * dst) {
+    KqkvShape s{};
+    if (check_kqkv(kcache, q, nullptr, dst, &s) != MLA_M4_OK) return 0;
+    const int sp = default_splits(s);
+    return sp > 1 ? part_bytes(s, sp) : 0;
+}
+
+int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type) {
+    if (n_kv < 1 || n_head < 1) return MLA_M4_ERR_ARG;
+    KqkvShape s{};
+    s.dk = 576; s.dv = 512; s.n_kv = n_kv; s.n_head = n_head; s.nt = 1; s.kc_type = kcache_type;
+    return default_splits(s);
+}
+
+int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask, float kq_scale,
+                const mla_m4_tensor * dst, void * workspace, size_t workspace_bytes, void * stream) {
+    KqkvShape s{};
+    int rc = check_kqkv(kcache, q, mask, dst, &s);
+    if (rc != MLA_M4_OK) return rc;
+    if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
+    const int sp = default_splits(s);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, sp);
+    if (sp == 1) {
+        a.dst = static_cast<float *>(dst->data);
+        return launch_attn(s, a, st);
+    }
+    if (!workspace || !aligned16(workspace) || workspace_bytes < part_bytes(s, sp)) return MLA_M4_ERR_WORKSPACE;
+    a.part = static_cast<float *>(workspace);
+    rc = launch_attn(s, a, st);
+    if (rc != MLA_M4_OK) return rc;
+    return mla::launch_merge(a.part, (int)s.dv, sp, (int)s.nt, (int)s.n_head, static_cast<float *>(dst->data), st) == hipSuccess
+               ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
+int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask,
+                        float kq_scale, int n_split, const mla_m4_tensor * part, void * stream) {
+    if (!part || !part->data) return MLA_M4_ERR_NULL;
+    // validate the attention operands against a synthetic dst view of the merged output
+    mla_m4_tensor dview{};
+    dview.data = part->data;
+    dview.type = MLA_M4_TYPE_F32;
+    dview.ne[0] = part->ne[0] - MLA_M4_PART_HDR;
+    dview.ne[1] = part->ne[2];
+    dview.ne[2] = part->ne[3];
+    dview.ne[3] = 1;
+    dview.nb[0] = 4;
+    dview.nb[1] = 4 * (size_t)dview.ne[0];
+    dview.nb[2] = dview.nb[1] * (size_t)dview.ne[1];
+    dview.nb[3] = dview.nb[2] * (size_t)dview.ne[2];
+    KqkvShape s{};
+    int rc = check_kqkv(kcache, q, mask, &dview, &s);
+    if (rc != MLA_M4_OK) return rc;
+    if (n_split < 1 || n_split > MLA_M4_MAX_SPLITS) return MLA_M4_ERR_ARG;
+    if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
+    if (part->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
+    if (part->ne[1] != n_split || part->ne[2] != s.nt || part->ne[3] != s.n_head) return MLA_M4_ERR_SHAPE;
+    if (!is_contiguous(part) || !aligned16(part->data)) return MLA_M4_ERR_STRIDE;
+    mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, n_split);
+    a.part = static_cast<float *>(part->data);
+    return launch_attn(s, a, static_cast<hipStream_t>(stream));
+}
+
+int mla_m4_phase_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, void * stream) {
+    const int rc = check_merge(part, dst);
+    if (rc != MLA_M4_OK) return rc;
+    return mla::launch_merge(static_cast<const float *>(part->data), (int)(part->ne[0] - MLA_M4_PART_HDR),
+                             (int)part->ne[1], (int)part->ne[2], (int)part->ne[3],
+                             static_cast<float *>(dst->data), static_cast<hipStream_t>(stream)) == hipSuccess
+               ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
+int mla_m4_supports_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope, const mla_m4_tensor * dst) {
+    return check_wkb(w, q_nope, dst) == MLA_M4_OK;
+}
+
+int mla_m4_supports_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask,
+                         const mla_m4_tensor * dst) {
+    KqkvShape s{};
+    return check_kqkv(kcache, q, mask, dst, &s) == MLA_M4_OK;
+}
+
+int mla_m4_supports_phase(int32_t phase, const mla_m4_tensor * src0, const mla_m4_tensor * dst) {
+    if (phase == MLA_M4_PHASE_MERGE) return check_merge(src0, dst) == MLA_M4_OK;
+    return 0;   // phases 0 (KV-write) and 1 (wv_b) are not implemented by this library yet
+}
+
+int mla_m4_resolve_flag(int flag, int gpu_core) {
+    if (flag == -1) return gpu_core ? 1 : 0;
+    if (flag == 0) return 0;
+    if (flag == 1) return gpu_core ? 1 : MLA_M4_ERR_ARG;
+    return MLA_M4_ERR_ARG;
+}
+
+}  // extern "C"

@@ -1,0 +1,236 @@
+"""Python mirror of aubier's three custom ggml ops, calling the gfx950 kernels through the C ABI
+of include/mla_m4.h (aubier_amd/libmla_m4.so).
+
+Names and argument meaning follow the reference's op builders (vendor/llama.cpp/ggml/include/
+ggml.h:1524-1586, ggml.c:3405-3539): ``ggml_m4_wkb(w_kb, q_nope)``, ``ggml_m4_kqkv(kcache, q,
+mask, kq_scale)`` and the PHASE op's split-K merge ``ggml_m4_phase_merge(part)``.  A contract
+violation raises :class:`MlaM4Error` (the ggml glue aborts instead, keeping the FATAL semantics).
+There is no CPU path: without the built library every call raises.
+
+Tensors are torch CUDA tensors in row-major order, i.e. with the ggml ``ne[]`` axes reversed:
+
+=============  =========================  ==============================
+op / operand   ggml ne (fastest first)    torch shape
+=============  =========================  ==============================
+W_kb           [d_n, D_v, H]              [H, D_v, d_n]
+q_nope         [d_n, H, nt]               [nt, H, d_n] (a strided view is fine)
+WKB dst        [D_v, H, nt]               [nt, H, D_v] (a view into Qcur is fine)
+kcache         [D_k, n_kv]                [n_kv, D_k]  (f16 or f32)
+q (Qcur)       [D_k, H, nt]               [nt, H, D_k]
+mask           [n_kv, >= nt]              [>= nt, n_kv]
+KQKV dst       [D_v, nt, H]               [H, nt, D_v]
+partials       [4 + D_v, S, nt, H]        [H, nt, S, 4 + D_v]
+=============  =========================  ==============================
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libmla_m4.so"
+
+TYPE_F32, TYPE_F16 = 0, 1
+PART_HDR = 4
+MAX_SPLITS = 1024
+PHASE_KVWRITE, PHASE_WVB, PHASE_MERGE = 0, 1, 2
+
+STATUS = {
+    0: "ok", -1: "null tensor or data pointer", -2: "unsupported element type",
+    -3: "shape violates the op contract", -4: "strides/alignment violate the op contract",
+    -5: "workspace missing or too small", -6: "scalar argument out of range",
+    -7: "HIP launch failed", -8: "shape not implemented by these kernels",
+}
+
+
+class MlaM4Error(RuntimeError):
+    def __init__(self, op: str, status: int):
+        self.status = status
+        super().__init__(f"{op}: {STATUS.get(status, 'unknown status')} ({status})")
+
+
+class MlaTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("pad_", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_size_t * 4),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+_EXPORTS = {
+    "mla_m4_version": (ctypes.c_char_p, []),
+    "mla_m4_status_str": (ctypes.c_char_p, [ctypes.c_int]),
+    "mla_m4_wkb": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_void_p]),
+    "mla_m4_kqkv": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_float, ctypes.POINTER(MlaTensor),
+                                                                      ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mla_m4_kqkv_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(MlaTensor)] * 3),
+    "mla_m4_kqkv_default_splits": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
+    "mla_m4_kqkv_partial": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_float, ctypes.c_int,
+                                                                              ctypes.POINTER(MlaTensor), ctypes.c_void_p]),
+    "mla_m4_phase_merge": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 2 + [ctypes.c_void_p]),
+    "mla_m4_supports_wkb": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3),
+    "mla_m4_supports_kqkv": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 4),
+    "mla_m4_supports_phase": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(MlaTensor), ctypes.POINTER(MlaTensor)]),
+    "mla_m4_resolve_flag": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
+}
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libmla_m4.so (raises if it has not been built: there is no fallback path)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built (python -m aubier_amd.build); the MLA ops have no CPU path")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in _EXPORTS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_EXPORTS)
+
+
+# ------------------------------------------------------------------------------------ views
+_DT = {torch.float32: (TYPE_F32, 4), torch.float16: (TYPE_F16, 2)}
+
+
+def view(t: Optional[torch.Tensor]) -> Optional[MlaTensor]:
+    """ggml-style view of a torch tensor: ne/nb are the reversed shape/strides (bytes)."""
+    if t is None:
+        return None
+    if t.dtype not in _DT:
+        raise MlaM4Error("view", -2)
+    if t.dim() > 4:
+        raise MlaM4Error("view", -3)
+    ty, es = _DT[t.dtype]
+    v = MlaTensor()
+    v.data = t.data_ptr()
+    v.type = ty
+    shape = list(reversed(t.shape))
+    strides = [s * es for s in reversed(t.stride())]
+    while len(shape) < 4:
+        shape.append(1)
+        strides.append(strides[-1] * shape[-2] if strides else es)
+    for i in range(4):
+        v.ne[i] = int(shape[i])
+        v.nb[i] = int(strides[i])
+    return v
+
+
+def _ptr(v: Optional[MlaTensor]):
+    return ctypes.byref(v) if v is not None else None
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check(op: str, rc: int) -> None:
+    if rc != 0:
+        raise MlaM4Error(op, rc)
+
+
+# ------------------------------------------------------------------------------------ ops
+def ggml_m4_wkb(w_kb: torch.Tensor, q_nope: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GGML_OP_M4_WKB: out[t, h, c] = sum_d w_kb[h, c, d] * q_nope[t, h, d] (f32).
+
+    w_kb [H, D_v, d_n] contiguous; q_nope [nt, H, d_n] (strided view ok); out [nt, H, D_v]
+    (a view into the Qcur buffer ok)."""
+    lib = load_library()
+    if out is None:
+        out = torch.empty((q_nope.shape[0], w_kb.shape[0], w_kb.shape[1]), dtype=torch.float32, device=q_nope.device)
+    vw, vq, vo = view(w_kb), view(q_nope), view(out)
+    _check("ggml_m4_wkb", lib.mla_m4_wkb(_ptr(vw), _ptr(vq), _ptr(vo), _stream(q_nope)))
+    return out
+
+
+def kqkv_workspace_bytes(kcache: torch.Tensor, q: torch.Tensor, out: torch.Tensor) -> int:
+    lib = load_library()
+    return int(lib.mla_m4_kqkv_workspace_bytes(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(out))))
+
+
+def ggml_m4_kqkv(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[torch.Tensor], kq_scale: float,
+                 out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GGML_OP_M4_KQKV: out[h, t, :] = softmax_j(kq_scale * q[t, h] . K[j] + mask[t, j]) . V[j, :D_v].
+
+    kcache [n_kv, D_k] f16/f32; q [nt, H, D_k] f32; mask [>= nt, n_kv] f32 or None;
+    out [H, nt, D_v] f32 (D_v = 512 unless out is given).  workspace: optional uint8 device
+    buffer (allocated here when None and the shape needs one)."""
+    lib = load_library()
+    if out is None:
+        dv = 512 if kcache.shape[1] == 576 else (256 if kcache.shape[1] == 320 else kcache.shape[1])
+        out = torch.empty((q.shape[1], q.shape[0], dv), dtype=torch.float32, device=q.device)
+    vk, vq, vm, vo = view(kcache), view(q), view(mask), view(out)
+    need = int(lib.mla_m4_kqkv_workspace_bytes(_ptr(vk), _ptr(vq), _ptr(vo)))
+    if workspace is None and need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("ggml_m4_kqkv", lib.mla_m4_kqkv(_ptr(vk), _ptr(vq), _ptr(vm), ctypes.c_float(kq_scale), _ptr(vo),
+                                           ws_ptr, ws_bytes, _stream(q)))
+    return out
+
+
+def ggml_m4_kqkv_partial(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[torch.Tensor], kq_scale: float,
+                         n_split: int, part: Optional[torch.Tensor] = None, d_v: int = 512) -> torch.Tensor:
+    """Split-K pass 1 with an explicit split count: part [H, nt, n_split, 4 + D_v]."""
+    lib = load_library()
+    if part is None:
+        part = torch.empty((q.shape[1], q.shape[0], n_split, PART_HDR + d_v), dtype=torch.float32, device=q.device)
+    _check("ggml_m4_kqkv_partial", lib.mla_m4_kqkv_partial(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(mask)),
+                                                           ctypes.c_float(kq_scale), int(n_split), _ptr(view(part)),
+                                                           _stream(q)))
+    return part
+
+
+def ggml_m4_phase_merge(part: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GGML_OP_M4_PHASE phase 2: the split-K merge.  part [H, nt, S, 4 + D_v] -> out [H, nt, D_v]."""
+    lib = load_library()
+    if out is None:
+        out = torch.empty((part.shape[0], part.shape[1], part.shape[3] - PART_HDR), dtype=torch.float32,
+                          device=part.device)
+    _check("ggml_m4_phase_merge", lib.mla_m4_phase_merge(_ptr(view(part)), _ptr(view(out)), _stream(part)))
+    return out
+
+
+def default_splits(n_kv: int, n_head: int = 32, kcache_type: int = TYPE_F16) -> int:
+    return int(load_library().mla_m4_kqkv_default_splits(n_kv, n_head, kcache_type))
+
+
+def supports_kqkv(kcache, q, mask, out) -> bool:
+    lib = load_library()
+    return bool(lib.mla_m4_supports_kqkv(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(mask)), _ptr(view(out))))
+
+
+def supports_wkb(w_kb, q_nope, out) -> bool:
+    lib = load_library()
+    return bool(lib.mla_m4_supports_wkb(_ptr(view(w_kb)), _ptr(view(q_nope)), _ptr(view(out))))
+
+
+def supports_phase(phase: int, src0, dst) -> bool:
+    lib = load_library()
+    return bool(lib.mla_m4_supports_phase(int(phase), _ptr(view(src0)), _ptr(view(dst))))
+
+
+def resolve_flag(flag: int, gpu_core: bool) -> bool:
+    """The tri-state enable flag (-1 AUTO, 0 off, 1 explicit); explicit without gpu_core raises."""
+    rc = int(load_library().mla_m4_resolve_flag(int(flag), int(bool(gpu_core))))
+    if rc < 0:
+        raise MlaM4Error("resolve_flag", rc)
+    return bool(rc)
+
+
+def kq_scale_default(d_k_nope: int = 128, d_rope: int = 64) -> float:
+    return 1.0 / math.sqrt(d_k_nope + d_rope)

@@ -1,0 +1,215 @@
+"""MLA decode attention benchmark on one MI355X (BASELINE.json metric: us per decode step plus
+achieved HBM GB/s as a fraction of peak, at 32,768 keys).
+
+    python bench.py [--steps K] [--warmup W] [--config 3] [--splits S] [--no-cpu]
+
+One step = the MLA attention of one decode token: GGML_OP_M4_WKB (absorbed q_nope written into
+the Qcur buffer) -> GGML_OP_M4_KQKV pass 1 (split-K partials) -> GGML_OP_M4_PHASE merge, through
+the C ABI, on seeded synthetic inputs (aubier_amd.inputs).  The steps are captured in a hipGraph
+(the way the engine runs them) and replayed; consecutive steps read different copies of the KV
+cache and W_kb (12 copies > the 256 MB MALL), so every step streams from HBM (COLD).
+
+Prints ONE JSON line.  `roofline` is for the dominant kernel (the split-K partial): algorithmic
+bytes per launch (n_kv * (1152 cache + 4 mask) + Qcur) / its average duration, timed with HIP
+events around a graph of back-to-back launches on the stream they run on.  `cpu_baseline` is the
+CPU oracle (the restated unfused ggml graph) on all host cores, same inputs, median of 5.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "µs/decode-step + achieved HBM GB/s (% peak) for MLA attention at 32K keys"
+HBM_PEAK_GBPS = 8000.0
+N_ROT = 12
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--splits", type=int, default=0, help="split count (0 = library default)")
+    ap.add_argument("--sweep", action="store_true", help="also time S in {64,128,192,256}")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--warm", action="store_true", help="also report WARM (one cache) timings")
+    return ap.parse_args()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the split-K decode path runs on a single "
+              "MI355X); multi-GPU runs are not part of it.", file=sys.stderr)
+        return 2
+    import torch
+    import aubier_amd as A
+    from aubier_amd import inputs as I
+
+    dev = torch.device("cuda:0")
+    A.load_library()
+    inp = I.make_config(args.config)
+    H, DV, DK = I.N_HEAD, I.D_V, I.D_K
+    W = inp.n_kv
+    es = 2 if inp.kc_f16 else 4
+
+    # ---- device buffers: N_ROT copies of the per-layer data (cache, W_kb, q) ----
+    kc0 = torch.from_numpy(np.ascontiguousarray(inp.kcache)).to(dev)
+    wkb0 = torch.from_numpy(inp.w_kb).to(dev)
+    q = np.zeros((inp.nt, H, I.D_NOPE + I.D_ROPE), dtype=np.float32)
+    q[:, :, :I.D_NOPE] = inp.q_nope
+    q[:, :, I.D_NOPE:] = inp.q_pe
+    q0 = torch.from_numpy(q).to(dev)
+    mask = torch.from_numpy(inp.mask).to(dev)
+    kcs = [kc0] + [kc0.clone() for _ in range(N_ROT - 1)]
+    wkbs = [wkb0] + [wkb0.clone() for _ in range(N_ROT - 1)]
+    qs = [q0] + [q0.clone() for _ in range(N_ROT - 1)]
+    qcurs = []
+    for i in range(N_ROT):
+        qc = torch.zeros((inp.nt, H, DK), dtype=torch.float32, device=dev)
+        qc[:, :, DV:] = qs[i][:, :, I.D_NOPE:]
+        qcurs.append(qc)
+    S = args.splits or A.default_splits(W, H, A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32)
+    part = torch.empty((H, inp.nt, S, A.ops.PART_HDR + DV), dtype=torch.float32, device=dev)
+    out = torch.empty((H, inp.nt, DV), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def wkb(i):
+        A.ggml_m4_wkb(wkbs[i], qs[i][:, :, :I.D_NOPE], out=qcurs[i][:, :, :DV])
+
+    def attn(i, part_=None, S_=None):
+        A.ggml_m4_kqkv_partial(kcs[i], qcurs[i], mask, inp.kq_scale, S_ or S, part=part_ if part_ is not None else part)
+
+    def merge(part_=None):
+        A.ggml_m4_phase_merge(part_ if part_ is not None else part, out=out)
+
+    def step(i):
+        wkb(i)
+        attn(i)
+        merge()
+
+    def capture(fn, n):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(2):            # untimed eager warmup on the capture stream
+                fn(i % N_ROT)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i % N_ROT)
+        return g
+
+    def time_graph(g, reps, per):
+        """us per unit: replay g `reps` times (each replay = `per` units) between two events."""
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (reps * per)
+
+    # ---- the timed region: K steps, graph-captured in blocks of N_ROT ----
+    g_step = capture(step, N_ROT)
+    reps = max(1, args.steps // N_ROT)
+    K = reps * N_ROT
+    for _ in range(max(1, args.warmup // N_ROT)):
+        g_step.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        g_step.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us_step = e0.elapsed_time(e1) * 1000.0 / K
+
+    # ---- per-kernel durations (graphs of back-to-back launches of one kernel, COLD) ----
+    per_reps = max(4, reps)
+    us_wkb = time_graph(capture(wkb, N_ROT), per_reps, N_ROT)
+    us_attn = time_graph(capture(attn, N_ROT), per_reps, N_ROT)
+    us_merge = time_graph(capture(lambda i: merge(), N_ROT), per_reps, N_ROT)
+
+    bytes_attn = W * (DK * es + 4) + inp.nt * H * DK * 4              # cache + mask + Qcur
+    bytes_wkb = H * DV * I.D_NOPE * 4 + inp.nt * H * I.D_NOPE * 4 + inp.nt * H * DV * 4
+    bytes_step_alg = bytes_attn + inp.nt * H * DV * 4 + bytes_wkb     # + final output
+    gbps_attn = bytes_attn / (us_attn * 1e3)
+    gbps_step = bytes_step_alg / (us_step * 1e3)
+
+    extra = {
+        "us_wkb": round(us_wkb, 3), "us_kqkv_partial": round(us_attn, 3), "us_phase_merge": round(us_merge, 3),
+        "step_GBps": round(gbps_step, 1), "step_frac_of_hbm_peak": round(gbps_step / HBM_PEAK_GBPS, 4),
+        "wkb_GBps": round(bytes_wkb / (us_wkb * 1e3), 1),
+        "partial_bytes": int(part.numel() * 4), "alg_bytes_step": int(bytes_step_alg),
+        "wall_s_timed": round(wall, 3),
+    }
+    if args.sweep:
+        sweep = {}
+        for S_ in (64, 128, 192, 256):
+            p_ = torch.empty((H, inp.nt, S_, A.ops.PART_HDR + DV), dtype=torch.float32, device=dev)
+            ua = time_graph(capture(lambda i, p_=p_, S_=S_: attn(i, p_, S_), N_ROT), per_reps, N_ROT)
+            um = time_graph(capture(lambda i, p_=p_: merge(p_), N_ROT), per_reps, N_ROT)
+            sweep[str(S_)] = {"us_partial": round(ua, 3), "us_merge": round(um, 3),
+                              "partial_GBps": round(bytes_attn / (ua * 1e3), 1)}
+        extra["split_sweep"] = sweep
+    if args.warm:
+        g_w = capture(lambda i: step(0), N_ROT)
+        extra["warm_us_step"] = round(time_graph(g_w, per_reps, N_ROT), 3)
+
+    # ---- CPU baseline: the restated unfused ggml graph on the host cores (rank 0, N=1) ----
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        nthr = min(os.cpu_count() or 1, 16)
+        orc.mla_step(inp, threads=nthr)            # warm-up
+        ts = []
+        for _ in range(5):
+            t = time.perf_counter()
+            orc.mla_step(inp, threads=nthr)
+            ts.append(time.perf_counter() - t)
+        t1 = time.perf_counter()
+        orc.mla_step(inp, threads=1)
+        one = time.perf_counter() - t1
+        cpu = {"value": round(statistics.median(ts) * 1e6, 1), "unit": "us/step", "cores": nthr, "kind": "port",
+               "sample": f"config {args.config} full step (WKB + unfused kq/softmax/kqv), median of 5 after 1 warm-up",
+               "value_1thread": round(one * 1e6, 1)}
+
+    rec = {
+        "metric": METRIC, "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(us_step / 1000.0, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16" if inp.kc_f16 else "f32", "data": "synthetic",
+        "config": {"workload": f"config {args.config}: MLA decode, 1 token x 32 heads, {W} keys, "
+                               f"{'f16' if inp.kc_f16 else 'f32'} latent+rope cache [{W},576], W_kb f32 [32,512,128], "
+                               f"split-K S={S} + PHASE merge, COLD ({N_ROT} rotating copies), hipGraph",
+                   "n_kv": W, "n_head": H, "d_k": DK, "d_v": DV, "splits": S, "seeds": inp.seeds, "notes": inp.notes},
+        "roofline": {"bound": "hbm", "achieved": round(gbps_attn, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps_attn / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "kqkv_decode_f16_kernel<576,512>", "alg_bytes_per_launch": int(bytes_attn),
+                     "us_per_launch": round(us_attn, 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,166 @@
+/*
+ * mla_m4.h -- the C ABI of the MI355X (gfx950) MLA attention kernels behind aubier's three
+ * custom ggml ops GGML_OP_M4_WKB, GGML_OP_M4_KQKV and GGML_OP_M4_PHASE.
+ *
+ * The ggml HIP backend's launchers (ggml_cuda_m4_wkb / ggml_cuda_m4_kqkv / ggml_cuda_m4_phase,
+ * dispatched from ggml_cuda_compute_forward) fill the tensor views below from their ggml_tensor
+ * arguments and call these entry points on ctx.stream().  Every entry point:
+ *   - is a plain asynchronous launch on `stream` (a hipStream_t): no allocation, no stream or
+ *     device synchronisation, no host read of device memory -- legal inside hipGraph capture;
+ *   - validates the whole shape/type/stride contract on the host BEFORE launching and returns a
+ *     negative MLA_M4_ERR_* code on a violation (the ggml glue turns that into GGML_ABORT, which
+ *     keeps the reference's FATAL semantics);
+ *   - reports a failed launch through hipGetLastError as MLA_M4_ERR_LAUNCH.
+ * Thread-compatible: one stream per call; concurrent streams need separate workspaces.
+ *
+ * Axis order is ggml's (ne[0] fastest).  Geometry is taken from ne[]/nb[]: the kernels are
+ * instantiated for the two MLA geometries in use -- (D_k, D_v, d_n) = (576, 512, 128) and
+ * (320, 256, 64) -- and any head count.
+ */
+#ifndef MLA_M4_H
+#define MLA_M4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types.  The values are ggml's enum ggml_type numbers, so the glue passes
+ * tensor->type through unchanged. */
+enum {
+    MLA_M4_TYPE_F32  = 0,
+    MLA_M4_TYPE_F16  = 1,
+    MLA_M4_TYPE_Q8_0 = 8,
+    MLA_M4_TYPE_I32  = 26,
+    MLA_M4_TYPE_I64  = 27
+};
+
+/* Status codes. */
+enum {
+    MLA_M4_OK             =  0,
+    MLA_M4_ERR_NULL       = -1,  /* a required pointer is NULL */
+    MLA_M4_ERR_TYPE       = -2,  /* unsupported element type */
+    MLA_M4_ERR_SHAPE      = -3,  /* ne[] violates the op contract */
+    MLA_M4_ERR_STRIDE     = -4,  /* nb[] violates the op contract (alignment, overlap, permutation) */
+    MLA_M4_ERR_WORKSPACE  = -5,  /* workspace missing or smaller than mla_m4_kqkv_workspace_bytes() */
+    MLA_M4_ERR_ARG        = -6,  /* a scalar argument is out of range (split count, phase id, ...) */
+    MLA_M4_ERR_LAUNCH     = -7,  /* the HIP launch failed (hipGetLastError) */
+    MLA_M4_ERR_UNSUPPORTED = -8  /* a legal ggml shape these kernels do not implement */
+};
+
+/* A device tensor view: the data/type/ne/nb fields of a ggml_tensor (ggml.h struct ggml_tensor). */
+typedef struct mla_m4_tensor {
+    void *  data;    /* device pointer */
+    int32_t type;    /* MLA_M4_TYPE_* */
+    int32_t pad_;
+    int64_t ne[4];   /* elements per axis, fastest first */
+    size_t  nb[4];   /* byte strides per axis */
+} mla_m4_tensor;
+
+/* GGML_OP_M4_PHASE selectors (op_params[0]).  0 and 1 keep the reference's meaning
+ * (patches/ggml-m4/m4-phase.cuh:3-14); 2 is the split-K merge. */
+enum {
+    MLA_M4_PHASE_KVWRITE = 0,
+    MLA_M4_PHASE_WVB     = 1,
+    MLA_M4_PHASE_MERGE   = 2
+};
+
+/* Number of floats in front of the D_v accumulators in one split-K partial record:
+ * rec = { m (natural-log units), l, 0, 0, o[0..D_v) }.  A partial tensor is
+ * F32 ne [MLA_M4_PART_HDR + D_v, n_split, nt, H], contiguous. */
+#define MLA_M4_PART_HDR 4
+
+/* Largest split count mla_m4_kqkv_partial accepts. */
+#define MLA_M4_MAX_SPLITS 1024
+
+const char * mla_m4_version(void);
+const char * mla_m4_status_str(int status);
+
+/* -------------------------------------------------------------------------------------------
+ * GGML_OP_M4_WKB -- the MLA absorption of the query's nope half into the latent space.
+ * Replaces ggml_cuda_m4_wkb (patches/ggml-m4/m4-wkb.cu:71-86); builder contract ggml_m4_wkb
+ * (vendor/llama.cpp/ggml/src/ggml.c:3405-3426), generalised from the fixed Q8_0 [64,256,32]:
+ *   w      F32  ne [d_n, D_v, H]     contiguous (W_kb: W[h][c][d])
+ *   q_nope F32  ne [d_n, H, nt]      nb[0] = 4, any 16-byte-aligned head/token strides
+ *                                     (the engine's view of q with a (d_n + d_r)-float head stride)
+ *   dst    F32  ne [D_v, H, nt]      nb[0] = 4, 16-byte-aligned strides (may be a view into Qcur)
+ *   dst[t][h][c] = sum_d w[h][c][d] * q_nope[t][h][d]          (f32 throughout, as ggml-cpu)
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
+               const mla_m4_tensor * dst, void * stream);
+
+/* -------------------------------------------------------------------------------------------
+ * GGML_OP_M4_KQKV -- fused Q.K^T over the latent+rope KV cache, masked softmax, then .V.
+ * Replaces ggml_cuda_m4_kqkv (patches/ggml-m4/m4-kqkv.cu:340-378); builder contract
+ * ggml_m4_kqkv (ggml.c:3429-3460), generalised:
+ *   kcache F16|F32 ne [D_k, n_kv]    nb[0] = elsize, row stride nb[1] a multiple of 16 bytes;
+ *                                     K = all D_k columns, V = columns [0, D_v) of the same row
+ *   q      F32     ne [D_k, H, nt]   nb[0] = 4 (Qcur: absorbed nope part, then the rope part)
+ *   mask   F32     ne [n_kv, >= nt]  nb[0] = 4 (0 / -INFINITY per key and token), or data NULL
+ *   dst    F32     ne [D_v, nt, H]   contiguous
+ *   kq_scale = op_params[0]
+ *   dst[h][t][:] = softmax_j(kq_scale * q[t][h].K[j] + mask[t][j]) . V[j][:]
+ * An F16 cache runs on MFMA with q and P rounded to f16 (the rounding points of the unfused
+ * ggml-cpu graph, whose mul_mat converts src1 to F16 for an F16 src0); an F32 cache runs in f32.
+ * nt == 1 is split-K decode (partial + merge, two launches); nt > 1 is the prefill path.
+ * `workspace` (device memory, >= mla_m4_kqkv_workspace_bytes()) holds the split-K partials.
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
+                const mla_m4_tensor * mask, float kq_scale, const mla_m4_tensor * dst,
+                void * workspace, size_t workspace_bytes, void * stream);
+
+/* Workspace bytes mla_m4_kqkv needs for these shapes (0 when no partials are used). */
+size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
+                                   const mla_m4_tensor * dst);
+
+/* Split count mla_m4_kqkv uses for a decode window of n_kv keys (a function of the window). */
+int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type);
+
+/* -------------------------------------------------------------------------------------------
+ * Split-K pass 1 on its own: the partial kernel of patches/ggml-m4/m4-kqkv.cu:201-312 with an
+ * explicit split count (1 .. MLA_M4_MAX_SPLITS).  Keys are partitioned into n_split contiguous
+ * ranges of whole 64-key tiles, balanced (the first n_tiles % n_split ranges get one more).
+ *   part F32 ne [MLA_M4_PART_HDR + D_v, n_split, nt, H] contiguous.
+ * Followed by mla_m4_phase_merge this equals mla_m4_kqkv.
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
+                        const mla_m4_tensor * mask, float kq_scale, int n_split,
+                        const mla_m4_tensor * part, void * stream);
+
+/* -------------------------------------------------------------------------------------------
+ * GGML_OP_M4_PHASE, phase MLA_M4_PHASE_MERGE -- the split-K merge (the combine kernel of
+ * patches/ggml-m4/m4-kqkv.cu:314-338): m* = max m_s; l* = sum l_s e^(m_s - m*);
+ * o* = sum o_s e^(m_s - m*) over splits with m_s > -inf; dst = o* / l*, or 0 if every split is
+ * empty.
+ *   part F32 ne [MLA_M4_PART_HDR + D_v, n_split, nt, H] contiguous
+ *   dst  F32 ne [D_v, nt, H] contiguous
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_phase_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, void * stream);
+
+/* -------------------------------------------------------------------------------------------
+ * supports_op mirrors (ggml-cuda.cu:5848-5885): 1 if the entry point above accepts these
+ * tensors, 0 otherwise.  They run the same host-side contract checks as the launch, without
+ * launching, so the backend's supports_op and the launcher cannot disagree.
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_supports_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
+                        const mla_m4_tensor * dst);
+int mla_m4_supports_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
+                         const mla_m4_tensor * mask, const mla_m4_tensor * dst);
+int mla_m4_supports_phase(int32_t phase, const mla_m4_tensor * src0, const mla_m4_tensor * dst);
+
+/* -------------------------------------------------------------------------------------------
+ * The tri-state enable flag of each op (engine/m1_session.h:152-166, resolved at
+ * engine/m1_engine.cpp:2178-2197): flag -1 = AUTO (on iff the attention core runs on the GPU),
+ * 0 = off (the reference op sequence), 1 = explicit on, which requires gpu_core.  Returns 1/0
+ * for on/off, or MLA_M4_ERR_ARG for an explicit 1 without gpu_core or a flag outside {-1,0,1}
+ * (the engine CHECK-fails on that).
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_resolve_flag(int flag, int gpu_core);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLA_M4_H */

@@ -1,0 +1,194 @@
+"""TEST INFRASTRUCTURE ONLY: numpy-facing wrapper of oracle/libmla_oracle.so, the C restatement of
+the reference's unfused ggml CPU graph (see mla_oracle.c for what it restates, with file:line).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this module, as the
+checker or as the timed CPU baseline -- never as the product path.
+
+Array conventions are the torch/numpy (row-major, reversed ggml ne) shapes of aubier_amd.ops:
+kcache [n_kv, D_k] (float16 or float32), q [nt, H, D_k] f32, mask [nt, n_kv] f32 or None,
+KQKV out [H, nt, D_v], W_kb [H, D_v, d_n], q_nope [nt, H, d_n], WKB out [nt, H, D_v],
+partials [H, nt, S, 4 + D_v].
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libmla_oracle.so"
+_lib = None
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} not built (python -m aubier_amd.build --oracle)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.orc_randn.argtypes = [ctypes.c_uint64, _I64, ctypes.c_float, _P]
+        L.orc_f32_to_f16.argtypes = [_P, _P, _I64]
+        L.orc_f16_to_f32.argtypes = [_P, _P, _I64]
+        L.orc_kqkv.argtypes = [_P, _I32, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, ctypes.c_float,
+                               _I64, _P, ctypes.c_int, ctypes.c_int]
+        L.orc_kqkv.restype = ctypes.c_int
+        L.orc_attn_f64.argtypes = [_P, _I32, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, ctypes.c_float,
+                                   _I64, _P, ctypes.c_int]
+        L.orc_attn_f64.restype = ctypes.c_int
+        L.orc_partials.argtypes = [_P, _I32, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, ctypes.c_float,
+                                   _I64, _P, _I64, _P]
+        L.orc_partials.restype = ctypes.c_int
+        L.orc_merge.argtypes = [_P, _I64, _I64, _I64, _I64, _P, ctypes.c_int]
+        L.orc_merge.restype = ctypes.c_int
+        L.orc_wkb.argtypes = [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_int, ctypes.c_int]
+        L.orc_wkb.restype = ctypes.c_int
+        L.orc_kqkv_bench_pattern.argtypes = [_I64, _P, _I64, _P]
+        L.orc_max_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(_P)
+
+
+def _kc(kcache: np.ndarray):
+    if kcache.dtype == np.float16:
+        return 1, 2
+    if kcache.dtype == np.float32:
+        return 0, 4
+    raise TypeError(kcache.dtype)
+
+
+def randn(seed: int, n: int, scale: float = 0.05) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().orc_randn(seed, n, scale, _ptr(out))
+    return out
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().orc_f16_to_f32(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def kqkv(kcache: np.ndarray, q: np.ndarray, mask: Optional[np.ndarray], kq_scale: float, d_v: int = 512,
+         threads: Optional[int] = None, mutant: int = 0) -> np.ndarray:
+    """The unfused ggml graph kq -> soft_max_ext -> kqv (engine/m1_layer.cpp:477-495) on the CPU."""
+    kcache = np.ascontiguousarray(kcache)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    ty, es = _kc(kcache)
+    n_kv, d_k = kcache.shape
+    nt, H, _ = q.shape
+    out = np.empty((H, nt, d_v), dtype=np.float32)
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.float32)
+    rc = lib().orc_kqkv(_ptr(kcache), ty, d_k, n_kv, d_k * es, _ptr(q), H, nt, d_k * 4, H * d_k * 4,
+                        _ptr(mask), n_kv * 4, kq_scale, d_v, _ptr(out), threads or max_threads(), mutant)
+    assert rc == 0
+    return out
+
+
+def attn_f64(kcache: np.ndarray, q: np.ndarray, mask: Optional[np.ndarray], kq_scale: float, d_v: int = 512,
+             threads: Optional[int] = None) -> np.ndarray:
+    """Double-precision brute force (no f16 rounding of q or P)."""
+    kcache = np.ascontiguousarray(kcache)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    ty, es = _kc(kcache)
+    n_kv, d_k = kcache.shape
+    nt, H, _ = q.shape
+    out = np.empty((H, nt, d_v), dtype=np.float64)
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.float32)
+    rc = lib().orc_attn_f64(_ptr(kcache), ty, d_k, n_kv, d_k * es, _ptr(q), H, nt, d_k * 4, H * d_k * 4,
+                            _ptr(mask), n_kv * 4, kq_scale, d_v, _ptr(out), threads or max_threads())
+    assert rc == 0
+    return out
+
+
+def split_bounds(n_kv: int, n_split: int, tile: int = 64) -> np.ndarray:
+    """Key boundaries of the balanced whole-tile partition used by the split-K kernels."""
+    n_tiles = (n_kv + tile - 1) // tile
+    base, rem = divmod(n_tiles, n_split)
+    b = [0]
+    for s in range(n_split):
+        b.append(b[-1] + base + (1 if s < rem else 0))
+    return np.minimum(np.array(b, dtype=np.int64) * tile, n_kv)
+
+
+def partials(kcache: np.ndarray, q: np.ndarray, mask: Optional[np.ndarray], kq_scale: float, bounds: Sequence[int],
+             d_v: int = 512) -> np.ndarray:
+    kcache = np.ascontiguousarray(kcache)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    ty, es = _kc(kcache)
+    n_kv, d_k = kcache.shape
+    nt, H, _ = q.shape
+    b = np.ascontiguousarray(bounds, dtype=np.int64)
+    S = len(b) - 1
+    part = np.empty((H, nt, S, 4 + d_v), dtype=np.float32)
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.float32)
+    rc = lib().orc_partials(_ptr(kcache), ty, d_k, n_kv, d_k * es, _ptr(q), H, nt, d_k * 4, H * d_k * 4,
+                            _ptr(mask), n_kv * 4, kq_scale, d_v, _ptr(b), S, _ptr(part))
+    assert rc == 0
+    return part
+
+
+def merge(part: np.ndarray, mutant: int = 0) -> np.ndarray:
+    part = np.ascontiguousarray(part, dtype=np.float32)
+    H, nt, S, rs = part.shape
+    out = np.empty((H, nt, rs - 4), dtype=np.float32)
+    rc = lib().orc_merge(_ptr(part), rs - 4, S, nt, H, _ptr(out), mutant)
+    assert rc == 0
+    return out
+
+
+def wkb(w_kb: np.ndarray, q_nope: np.ndarray, threads: Optional[int] = None, mutant: int = 0) -> np.ndarray:
+    """The unfused WKB: permute(mul_mat(W_kb, permute(q_nope))) (engine/m1_layer.cpp:444-446)."""
+    w_kb = np.ascontiguousarray(w_kb, dtype=np.float32)
+    H, d_v, d_n = w_kb.shape
+    nt = q_nope.shape[0]
+    qn = np.ascontiguousarray(q_nope, dtype=np.float32)
+    out = np.empty((nt, H, d_v), dtype=np.float32)
+    rc = lib().orc_wkb(_ptr(w_kb), d_n, d_v, H, _ptr(qn), nt, d_n * 4, H * d_n * 4, _ptr(out), d_v * 4,
+                       H * d_v * 4, threads or max_threads(), mutant)
+    assert rc == 0
+    return out
+
+
+def kqkv_bench_pattern(n_kv: int, d_k: int = 320, n_head: int = 32):
+    """Known-answer inputs of engine/m1_kqkv_bench.hip:148-165 (kcache f16 [n_kv, d_k], q f32 [1, H, d_k])."""
+    kc = np.empty(n_kv * d_k, dtype=np.uint16)
+    q = np.empty(n_head * d_k, dtype=np.float32)
+    lib().orc_kqkv_bench_pattern(kc.size, _ptr(kc), q.size, _ptr(q))
+    return kc.view(np.float16).reshape(n_kv, d_k), q.reshape(1, n_head, d_k)
+
+
+def mla_step(inp, threads: Optional[int] = None) -> tuple[np.ndarray, np.ndarray]:
+    """The whole unfused decode/prefill step of a config: WKB, concat -> Qcur, KQKV.
+    Returns (qcur [nt, H, 576], out [H, nt, 512])."""
+    q_abs = wkb(inp.w_kb, inp.q_nope, threads=threads)
+    qcur = np.concatenate([q_abs, inp.q_pe], axis=2).astype(np.float32)
+    out = kqkv(inp.kcache, qcur, inp.mask, inp.kq_scale, d_v=inp.w_kb.shape[1], threads=threads)
+    return qcur, out
+
+
+os.environ.setdefault("OMP_WAIT_POLICY", "PASSIVE")
