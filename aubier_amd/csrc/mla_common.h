@@ -38,6 +38,16 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// gfx950 LDS transpose read (ds_read_b64_tr_b16).  In each 16-lane group, lane j supplies the
+// address of 4 consecutive 16-bit elements; the 16 addresses form a 4 x 16 block (lane j holds row
+// j >> 2, columns 4 (j & 3) .. +3) and lane j receives column j of that block, rows 0..3.
+typedef short short4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ half4 lds_read_tr16(const half_t * p) {
+    const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) short4v *)(__attribute__((address_space(3))) void *)p);
+    return __builtin_bit_cast(half4, v);
+}
+
 // 16-byte global load/store helpers
 __device__ __forceinline__ u32x4 ld16(const void * p) { return *reinterpret_cast<const u32x4 *>(p); }
 __device__ __forceinline__ u32x4 ld16_stream(const void * p) {

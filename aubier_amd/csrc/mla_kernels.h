@@ -7,6 +7,17 @@
 
 namespace mla {
 
+// Split-K partial block of one (32-head group, token, split), blocks ordered [group][token][split]:
+//   float m[32]        running max of the split's scores (natural-log units; -inf if empty)
+//   float l[32]        sum_j exp(s_j - m)
+//   T     o[32][D_v]   o / l: the split's normalised softmax output, 0 for an empty split.  T is
+//                      the cache's element type: f16 for an f16 cache (|o / l| <= max|V|, so it
+//                      cannot overflow), f32 for an f32 cache.
+constexpr int PART_HEADS = 32;
+__host__ __device__ constexpr size_t part_block_bytes(int dv, int o_bytes) {
+    return 256 + (size_t)PART_HEADS * (size_t)o_bytes * (size_t)dv;
+}
+
 // Split-K decode / generic attention launch arguments (byte strides throughout).
 struct DecodeArgs {
     const char * kc;        // cache base
@@ -21,7 +32,7 @@ struct DecodeArgs {
     int nt;
     int n_split;
     int n_tiles;            // ceil(n_kv / 64)
-    float * part;           // partial records (when dst == null)
+    char * part;            // partial blocks (when dst == null)
     float * dst;            // final output (single-split launches), contiguous [D_v, nt, H]
 };
 
@@ -32,8 +43,8 @@ bool decode_f16_supported(int dk, int dv);
 // (split, head, token).  round16 applies the f16 rounding of q and P (F16 cache semantics).
 hipError_t launch_kqkv_generic(int dk, int dv, int kc_is_f16, const DecodeArgs & a, hipStream_t stream);
 
-// Split-K merge: part [(4 + dv), n_split, nt, H] -> dst [dv, nt, H]
-hipError_t launch_merge(const float * part, int dv, int n_split, int nt, int n_head, float * dst,
+// Split-K merge: partial blocks [group][token][split] (o of o_bytes = 2 or 4) -> dst [dv, nt, H]
+hipError_t launch_merge(const char * part, int dv, int o_bytes, int n_split, int nt, int n_head, float * dst,
                         hipStream_t stream);
 
 // WKB: dst[t][h][c] = sum_d w[h][c][d] * q[t][h][d]

@@ -101,8 +101,14 @@ int default_splits(const KqkvShape & s) {
     return (int)sp;
 }
 
+int64_t n_groups_of(int64_t n_head) { return (n_head + MLA_M4_PART_HEADS - 1) / MLA_M4_PART_HEADS; }
+
+int part_o_bytes(const KqkvShape & s) { return s.kc_type == MLA_M4_TYPE_F16 ? 2 : 4; }
+
+int64_t part_floats(const KqkvShape & s) { return (int64_t)(mla::part_block_bytes((int)s.dv, part_o_bytes(s)) / 4); }
+
 size_t part_bytes(const KqkvShape & s, int n_split) {
-    return (size_t)s.n_head * (size_t)s.nt * (size_t)n_split * (size_t)(MLA_M4_PART_HDR + s.dv) * sizeof(float);
+    return (size_t)n_groups_of(s.n_head) * (size_t)s.nt * (size_t)n_split * mla::part_block_bytes((int)s.dv, part_o_bytes(s));
 }
 
 mla::DecodeArgs make_args(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_tensor * mask,
@@ -137,11 +143,13 @@ int launch_attn(const KqkvShape & s, const mla::DecodeArgs & a, hipStream_t stre
 int check_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst) {
     if (!part || !dst || !part->data || !dst->data) return MLA_M4_ERR_NULL;
     if (part->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
-    const int64_t dv = part->ne[0] - MLA_M4_PART_HDR;
-    if (dv < 4 || (dv & 3) || part->ne[1] < 1 || part->ne[1] > MLA_M4_MAX_SPLITS) return MLA_M4_ERR_SHAPE;
-    if (dst->ne[0] != dv || dst->ne[1] != part->ne[2] || dst->ne[2] != part->ne[3] || dst->ne[3] != 1)
+    const int64_t dv = dst->ne[0];
+    if (dv < 8 || (dv & 7) || dst->ne[1] < 1 || dst->ne[2] < 1 || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if ((part->ne[0] != MLA_M4_PART_FLOATS(dv) && part->ne[0] != MLA_M4_PART_FLOATS_F32(dv)) ||
+        part->ne[1] < 1 || part->ne[1] > MLA_M4_MAX_SPLITS ||
+        part->ne[2] != dst->ne[1] || part->ne[3] != n_groups_of(dst->ne[2]))
         return MLA_M4_ERR_SHAPE;
-    if (part->ne[2] > 65535 || part->ne[3] > 65535) return MLA_M4_ERR_UNSUPPORTED;
+    if (dst->ne[1] > 65535 || dst->ne[2] > 65535) return MLA_M4_ERR_UNSUPPORTED;
     if (!is_contiguous(part) || !is_contiguous(dst) || !aligned16(part->data) || !aligned16(dst->data))
         return MLA_M4_ERR_STRIDE;
     return MLA_M4_OK;
@@ -207,7 +215,7 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope, const mla_
 size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * dst) {
     KqkvShape s{};
     if (check_kqkv(kcache, q, nullptr, dst, &s) != MLA_M4_OK) return 0;
-    const int sp = default_splits(s);
+    const int sp = (s.dv & 7) ? 1 : default_splits(s);
     return sp > 1 ? part_bytes(s, sp) : 0;
 }
 
@@ -224,7 +232,7 @@ int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla
     int rc = check_kqkv(kcache, q, mask, dst, &s);
     if (rc != MLA_M4_OK) return rc;
     if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
-    const int sp = default_splits(s);
+    const int sp = (s.dv & 7) ? 1 : default_splits(s);     // the merge reads 8 columns at a time
     hipStream_t st = static_cast<hipStream_t>(stream);
     mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, sp);
     if (sp == 1) {
@@ -232,23 +240,24 @@ int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla
         return launch_attn(s, a, st);
     }
     if (!workspace || !aligned16(workspace) || workspace_bytes < part_bytes(s, sp)) return MLA_M4_ERR_WORKSPACE;
-    a.part = static_cast<float *>(workspace);
+    a.part = static_cast<char *>(workspace);
     rc = launch_attn(s, a, st);
     if (rc != MLA_M4_OK) return rc;
-    return mla::launch_merge(a.part, (int)s.dv, sp, (int)s.nt, (int)s.n_head, static_cast<float *>(dst->data), st) == hipSuccess
+    return mla::launch_merge(a.part, (int)s.dv, part_o_bytes(s), sp, (int)s.nt, (int)s.n_head, static_cast<float *>(dst->data), st) == hipSuccess
                ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
 }
 
 int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask,
-                        float kq_scale, int n_split, const mla_m4_tensor * part, void * stream) {
+                        float kq_scale, int n_split, int64_t d_v, const mla_m4_tensor * part, void * stream) {
     if (!part || !part->data) return MLA_M4_ERR_NULL;
-    // validate the attention operands against a synthetic dst view of the merged output
+    if (!q) return MLA_M4_ERR_NULL;
+    // validate the attention operands against a dst view of the merged output
     mla_m4_tensor dview{};
     dview.data = part->data;
     dview.type = MLA_M4_TYPE_F32;
-    dview.ne[0] = part->ne[0] - MLA_M4_PART_HDR;
-    dview.ne[1] = part->ne[2];
-    dview.ne[2] = part->ne[3];
+    dview.ne[0] = d_v;
+    dview.ne[1] = q->ne[2];
+    dview.ne[2] = q->ne[1];
     dview.ne[3] = 1;
     dview.nb[0] = 4;
     dview.nb[1] = 4 * (size_t)dview.ne[0];
@@ -257,22 +266,26 @@ int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q, c
     KqkvShape s{};
     int rc = check_kqkv(kcache, q, mask, &dview, &s);
     if (rc != MLA_M4_OK) return rc;
+    if ((s.dv & 7) != 0) return MLA_M4_ERR_SHAPE;
     if (n_split < 1 || n_split > MLA_M4_MAX_SPLITS) return MLA_M4_ERR_ARG;
     if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
     if (part->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
-    if (part->ne[1] != n_split || part->ne[2] != s.nt || part->ne[3] != s.n_head) return MLA_M4_ERR_SHAPE;
+    if (part->ne[0] != part_floats(s) || part->ne[1] != n_split || part->ne[2] != s.nt ||
+        part->ne[3] != n_groups_of(s.n_head))
+        return MLA_M4_ERR_SHAPE;
     if (!is_contiguous(part) || !aligned16(part->data)) return MLA_M4_ERR_STRIDE;
     mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, n_split);
-    a.part = static_cast<float *>(part->data);
+    a.part = static_cast<char *>(part->data);
     return launch_attn(s, a, static_cast<hipStream_t>(stream));
 }
 
 int mla_m4_phase_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, void * stream) {
     const int rc = check_merge(part, dst);
     if (rc != MLA_M4_OK) return rc;
-    return mla::launch_merge(static_cast<const float *>(part->data), (int)(part->ne[0] - MLA_M4_PART_HDR),
-                             (int)part->ne[1], (int)part->ne[2], (int)part->ne[3],
-                             static_cast<float *>(dst->data), static_cast<hipStream_t>(stream)) == hipSuccess
+    const int o_bytes = part->ne[0] == MLA_M4_PART_FLOATS(dst->ne[0]) ? 2 : 4;
+    return mla::launch_merge(static_cast<const char *>(part->data), (int)dst->ne[0], o_bytes, (int)part->ne[1],
+                             (int)dst->ne[1], (int)dst->ne[2], static_cast<float *>(dst->data),
+                             static_cast<hipStream_t>(stream)) == hipSuccess
                ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
 }
 

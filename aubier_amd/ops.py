@@ -19,7 +19,7 @@ kcache         [D_k, n_kv]                [n_kv, D_k]  (f16 or f32)
 q (Qcur)       [D_k, H, nt]               [nt, H, D_k]
 mask           [n_kv, >= nt]              [>= nt, n_kv]
 KQKV dst       [D_v, nt, H]               [H, nt, D_v]
-partials       [4 + D_v, S, nt, H]        [H, nt, S, 4 + D_v]
+partials       [64 + 16 D_v, S, nt, G]    [G, nt, S, 64 + 16 D_v]   (G = ceil(H / 32) head groups)
 =============  =========================  ==============================
 """
 from __future__ import annotations
@@ -34,8 +34,15 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libmla_m4.so"
 
 TYPE_F32, TYPE_F16 = 0, 1
-PART_HDR = 4
+PART_HEADS = 32
 MAX_SPLITS = 1024
+
+
+def part_floats(d_v: int, kc_f16: bool = True) -> int:
+    """4-byte words per split-K partial block (include/mla_m4.h MLA_M4_PART_FLOATS[_F32])."""
+    return 64 + (16 if kc_f16 else 32) * d_v
+
+
 PHASE_KVWRITE, PHASE_WVB, PHASE_MERGE = 0, 1, 2
 
 STATUS = {
@@ -72,7 +79,7 @@ _EXPORTS = {
                                                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "mla_m4_kqkv_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(MlaTensor)] * 3),
     "mla_m4_kqkv_default_splits": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
-    "mla_m4_kqkv_partial": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_float, ctypes.c_int,
+    "mla_m4_kqkv_partial": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_float, ctypes.c_int, ctypes.c_int64,
                                                                               ctypes.POINTER(MlaTensor), ctypes.c_void_p]),
     "mla_m4_phase_merge": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 2 + [ctypes.c_void_p]),
     "mla_m4_supports_wkb": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3),
@@ -185,24 +192,45 @@ def ggml_m4_kqkv(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[torch.Ten
 
 def ggml_m4_kqkv_partial(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[torch.Tensor], kq_scale: float,
                          n_split: int, part: Optional[torch.Tensor] = None, d_v: int = 512) -> torch.Tensor:
-    """Split-K pass 1 with an explicit split count: part [H, nt, n_split, 4 + D_v]."""
+    """Split-K pass 1 with an explicit split count: part [G, nt, n_split, 64 + 16 D_v] (f32 words)."""
     lib = load_library()
     if part is None:
-        part = torch.empty((q.shape[1], q.shape[0], n_split, PART_HDR + d_v), dtype=torch.float32, device=q.device)
+        G = (q.shape[1] + PART_HEADS - 1) // PART_HEADS
+        part = torch.empty((G, q.shape[0], n_split, part_floats(d_v, kcache.dtype == torch.float16)),
+                           dtype=torch.float32, device=q.device)
     _check("ggml_m4_kqkv_partial", lib.mla_m4_kqkv_partial(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(mask)),
-                                                           ctypes.c_float(kq_scale), int(n_split), _ptr(view(part)),
-                                                           _stream(q)))
+                                                           ctypes.c_float(kq_scale), int(n_split), int(d_v),
+                                                           _ptr(view(part)), _stream(q)))
     return part
 
 
-def ggml_m4_phase_merge(part: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """GGML_OP_M4_PHASE phase 2: the split-K merge.  part [H, nt, S, 4 + D_v] -> out [H, nt, D_v]."""
+def ggml_m4_phase_merge(part: torch.Tensor, out: Optional[torch.Tensor] = None, n_head: Optional[int] = None,
+                        d_v: int = 512) -> torch.Tensor:
+    """GGML_OP_M4_PHASE phase 2: the split-K merge.  part [G, nt, S, 64 + 16 D_v] -> out [H, nt, D_v]."""
     lib = load_library()
     if out is None:
-        out = torch.empty((part.shape[0], part.shape[1], part.shape[3] - PART_HDR), dtype=torch.float32,
-                          device=part.device)
+        H = n_head if n_head is not None else part.shape[0] * PART_HEADS
+        out = torch.empty((H, part.shape[1], d_v), dtype=torch.float32, device=part.device)
     _check("ggml_m4_phase_merge", lib.mla_m4_phase_merge(_ptr(view(part)), _ptr(view(out)), _stream(part)))
     return out
+
+
+def decode_partials(part, n_head: int, d_v: int = 512):
+    """Split a partial buffer (numpy/torch, [G, nt, S, 64 + 16 D_v] f32 words) into
+    m [H, nt, S], l [H, nt, S] and o_norm [H, nt, S, D_v] (float32 numpy arrays)."""
+    import numpy as np
+    p = part.detach().cpu().numpy() if isinstance(part, torch.Tensor) else np.asarray(part)
+    G, nt, S, W = p.shape
+    m = p[..., :PART_HEADS]                                      # [G, nt, S, 32]
+    l = p[..., PART_HEADS:2 * PART_HEADS]
+    o = np.ascontiguousarray(p[..., 64:])
+    if W == part_floats(d_v, True):
+        o = o.view(np.float16)
+    o = o.reshape(G, nt, S, PART_HEADS, d_v)
+    m = np.moveaxis(m, 3, 1).reshape(G * PART_HEADS, nt, S)[:n_head]
+    l = np.moveaxis(l, 3, 1).reshape(G * PART_HEADS, nt, S)[:n_head]
+    o = np.moveaxis(o, 3, 1).reshape(G * PART_HEADS, nt, S, d_v)[:n_head].astype(np.float32)
+    return m, l, o
 
 
 def default_splits(n_kv: int, n_head: int = 32, kcache_type: int = TYPE_F16) -> int:

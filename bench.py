@@ -81,7 +81,7 @@ def main() -> int:
         qc[:, :, DV:] = qs[i][:, :, I.D_NOPE:]
         qcurs.append(qc)
     S = args.splits or A.default_splits(W, H, A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32)
-    part = torch.empty((H, inp.nt, S, A.ops.PART_HDR + DV), dtype=torch.float32, device=dev)
+    part = torch.empty(((H + 31) // 32, inp.nt, S, A.ops.part_floats(DV)), dtype=torch.float32, device=dev)
     out = torch.empty((H, inp.nt, DV), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
@@ -164,7 +164,7 @@ def main() -> int:
     if args.sweep:
         sweep = {}
         for S_ in (64, 128, 192, 256):
-            p_ = torch.empty((H, inp.nt, S_, A.ops.PART_HDR + DV), dtype=torch.float32, device=dev)
+            p_ = torch.empty(((H + 31) // 32, inp.nt, S_, A.ops.part_floats(DV)), dtype=torch.float32, device=dev)
             ua = time_graph(capture(lambda i, p_=p_, S_=S_: attn(i, p_, S_), N_ROT), per_reps, N_ROT)
             um = time_graph(capture(lambda i, p_=p_: merge(p_), N_ROT), per_reps, N_ROT)
             sweep[str(S_)] = {"us_partial": round(ua, 3), "us_merge": round(um, 3),

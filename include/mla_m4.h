@@ -67,10 +67,18 @@ enum {
     MLA_M4_PHASE_MERGE   = 2
 };
 
-/* Number of floats in front of the D_v accumulators in one split-K partial record:
- * rec = { m (natural-log units), l, 0, 0, o[0..D_v) }.  A partial tensor is
- * F32 ne [MLA_M4_PART_HDR + D_v, n_split, nt, H], contiguous. */
-#define MLA_M4_PART_HDR 4
+/* Split-K partials.  One block per (32-head group g, token t, split s), blocks ordered
+ * [g][t][s]:
+ *   float m[32]          running max of the split's scaled, masked scores (natural-log units,
+ *                        -INFINITY for a split with no live key)
+ *   float l[32]          sum over the split's keys of exp(score - m)
+ *   T     o[32][D_v]     o / l: the split's normalised softmax output (0 for an empty split);
+ *                        T = f16 for an F16 cache (MLA_M4_PART_FLOATS(D_v) words per block),
+ *                        T = f32 for an F32 cache (MLA_M4_PART_FLOATS_F32(D_v) words per block)
+ * As a tensor: F32 ne [words per block, n_split, nt, ceil(H / 32)], contiguous. */
+#define MLA_M4_PART_HEADS 32
+#define MLA_M4_PART_FLOATS(dv) (64 + 16 * (dv))
+#define MLA_M4_PART_FLOATS_F32(dv) (64 + 32 * (dv))
 
 /* Largest split count mla_m4_kqkv_partial accepts. */
 #define MLA_M4_MAX_SPLITS 1024
@@ -122,11 +130,13 @@ int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type
  * Split-K pass 1 on its own: the partial kernel of patches/ggml-m4/m4-kqkv.cu:201-312 with an
  * explicit split count (1 .. MLA_M4_MAX_SPLITS).  Keys are partitioned into n_split contiguous
  * ranges of whole 64-key tiles, balanced (the first n_tiles % n_split ranges get one more).
- *   part F32 ne [MLA_M4_PART_HDR + D_v, n_split, nt, H] contiguous.
+ *   part F32 ne [MLA_M4_PART_FLOATS(D_v) (F16 cache) or MLA_M4_PART_FLOATS_F32(D_v) (F32 cache),
+ *                n_split, nt, ceil(H / 32)] contiguous (layout above);
+ *   D_v is the V width the partials are for (512 for the 576-wide cache, 256 for the 320-wide).
  * Followed by mla_m4_phase_merge this equals mla_m4_kqkv.
  * ------------------------------------------------------------------------------------------- */
 int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
-                        const mla_m4_tensor * mask, float kq_scale, int n_split,
+                        const mla_m4_tensor * mask, float kq_scale, int n_split, int64_t d_v,
                         const mla_m4_tensor * part, void * stream);
 
 /* -------------------------------------------------------------------------------------------
@@ -134,8 +144,8 @@ int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
  * patches/ggml-m4/m4-kqkv.cu:314-338): m* = max m_s; l* = sum l_s e^(m_s - m*);
  * o* = sum o_s e^(m_s - m*) over splits with m_s > -inf; dst = o* / l*, or 0 if every split is
  * empty.
- *   part F32 ne [MLA_M4_PART_HDR + D_v, n_split, nt, H] contiguous
- *   dst  F32 ne [D_v, nt, H] contiguous
+ *   part F32 ne [MLA_M4_PART_FLOATS(D_v) or MLA_M4_PART_FLOATS_F32(D_v), n_split, nt, ceil(H / 32)]
+ *   dst  F32 ne [D_v, nt, H] contiguous (H and D_v are taken from dst; the o type from ne[0])
  * ------------------------------------------------------------------------------------------- */
 int mla_m4_phase_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, void * stream);
 

@@ -29,6 +29,6 @@ def run_step(g, kq_scale, n_split=None):
         out = A.ggml_m4_kqkv(g["kcache"], g["qcur"], g["mask"], kq_scale)
     else:
         part = A.ggml_m4_kqkv_partial(g["kcache"], g["qcur"], g["mask"], kq_scale, n_split)
-        out = A.ggml_m4_phase_merge(part)
+        out = A.ggml_m4_phase_merge(part, n_head=g["q"].shape[1])
     torch.cuda.synchronize()
     return g["qcur"].cpu().numpy(), out.cpu().numpy()
