@@ -8,24 +8,22 @@
 //     60 FLOP per cache byte): they run on v_mfma_f32_16x16x32_f16 / v_mfma_f32_32x32x16_f16 with
 //     f32 accumulation.  q and P enter the MFMA as f16 -- the same rounding points as the unfused
 //     ggml-cpu graph, whose mul_mat converts src1 to F16 for an F16 src0.
-//   * The cache streams through 64-key tiles: coalesced 16-byte nontemporal loads into a register
-//     double buffer keep tiles i+1 and i+2 in flight while tile i is computed out of LDS (rows
-//     padded by 16 bytes so the MFMA operand reads are bank-conflict free).
-//   * LDS traffic is the per-tile cost that matters, so every tile byte is read from LDS once by
-//     Q.K^T: the contraction over D_k is split between two waves (each holds the f16 q fragments
-//     of its D_k half for all 32 heads in registers), and the two half-scores are summed through a
-//     1 KB-per-wave exchange.
-//   * Online softmax in log2 units (v_exp_f32), rescaling the accumulators only by the per-tile
-//     factor; all-masked prefixes are guarded (no exp(-inf - -inf)).
+//   * Work split of a 64-key tile over the 4 waves (one per SIMD): for Q.K^T wave w owns keys
+//     16 w .. 16 w + 15 against all 32 heads (q fragments held in VGPRs); for P.V wave w owns the
+//     output columns D_v/4 * w .. + D_v/4 against all 64 keys (accumulators in AGPRs).  P moves
+//     between the two through a 4.5 KB LDS exchange, the only workgroup barrier per tile.
+//   * Each wave's key slices stream into a two-stage LDS ring by bounds-checked LDS DMA
+//     (buffer_load_dwordx4 ... lds: no staging registers, keys past n_kv read as zeros).  The stage
+//     layout (below) makes the Q.K^T operand reads and the transposed V reads (ds_read_b64_tr_b16)
+//     bank-conflict free and each a lane-invariant base plus an immediate offset.
+//   * Online softmax in log2 units (v_exp_f32) against a reference max shared by the waves and
+//     moved lazily: only when a tile raises a head's max by more than 2^8, so P = exp2(s - m_ref)
+//     <= 256 (exact range in f16) and the accumulator rescale is rare.  P is computed against the
+//     current reference before the barrier and recomputed after it only when the reference moves.
 //
-// Work split: grid = (n_split, ceil(H/32), nt), 256 threads = 4 waves, one per SIMD, so each wave
-// has the whole 512-entry register file (q fragments, two in-flight tiles, output accumulators).
-//   QK role:   wave w -> keys [32 kg, 32 kg + 32) (kg = w & 1) x all 32 heads over the D_k half
-//              dh = w >> 1; afterwards the wave owns the scores of head tile dh for its 32 keys
-//   PV role:   wave w -> output columns [w*D_v/4, (w+1)*D_v/4), all 32 heads
-// Output: one partial block per (32-head group, token, split) -- m and l per head in f32 and the
-// split's normalised output o/l in f16 (see mla_kernels.h) -- or, when the launch has a single
-// split, the final o/l in f32 written to dst.
+// Grid = (n_split, ceil(H/32), nt), 256 threads.  Output: one partial block per (32-head group,
+// token, split) -- m (the split's exact max) and l per head in f32 and the split's normalised
+// output o/l in f16, [32 heads][D_v] (mla_kernels.h) -- or, with a single split, o/l in f32 to dst.
 #include "mla_common.h"
 #include "mla_kernels.h"
 
@@ -33,292 +31,390 @@ namespace mla {
 
 namespace {
 
-constexpr int TK = 64;          // keys per tile
-constexpr int NWAVE = 4;        // one wavefront per SIMD: the 512-entry register file per lane
+constexpr int TK = 64;          // keys per split tile (splits are whole tiles)
+constexpr int NWAVE = 4;
 constexpr int NTHR = 64 * NWAVE;
+constexpr int WK = TK / NWAVE;  // keys per wave slice
 constexpr int HG = 32;          // heads per workgroup
+constexpr float LAZY = 8.0f;    // log2 slack before the reference max moves
 
 template <int DK, int DV>
 struct DecodeCfg {
-    static_assert(DK % 64 == 0 && DV % 256 == 0 && DV <= DK, "geometry");
-    static constexpr int KROW = DK + 8;                 // LDS row pitch in halves (+16 bytes)
+    static_assert(DK % 64 == 0 && DV % 128 == 0 && DV <= DK, "geometry");
     static constexpr int CH = DK * 2 / 16;              // 16-byte chunks per cache row
-    static constexpr int NCHUNK = TK * CH;
-    static constexpr int NPT = NCHUNK / NTHR;           // staged chunks per thread per tile
-    static constexpr int QCH = HG * DK / 4;             // 16-byte f32 chunks of the WG's q block
-    static constexpr int QPT = QCH / NTHR;              // q chunks per thread
-    static constexpr int HSTEPS = DK / 64;              // 16x16x32 K-steps per D_k half
-    static constexpr int DVW = DV / NWAVE;              // output columns per wave
-    static constexpr int NT_DV = DVW / 32;              // 32-wide MFMA tiles per wave
-    static constexpr int PROW = TK + 8;                 // P row pitch in halves
-    static constexpr int OCH = HG * DV / 8;             // 16-byte f16 chunks of the WG's output block
-    static constexpr int OPT = OCH / NTHR;
-    static_assert(NCHUNK % NTHR == 0 && QCH % NTHR == 0 && OCH % NTHR == 0, "whole chunks per thread");
-    static_assert(HG * DV * 2 <= TK * KROW * 2, "f16 output block fits the tile buffer");
+    static_assert(CH % 4 == 0, "1 KB stage blocks of 4 chunks x 16 rows");
+    static constexpr int DMA_N = WK * CH / 64;          // 16-byte DMA instructions per slice
+    static constexpr int ROWS_BYTES = WK * DK * 2;
+    static constexpr int STAGE = ROWS_BYTES + 256;      // 16 K rows + the mask slot
+    static constexpr int RING = 2 * NWAVE * STAGE;
+    static constexpr int QSTEPS = DK / 32;              // K-steps of the 16x16x32 MFMA
+    static constexpr int DVQ = DV / NWAVE;              // output columns per wave
+    static constexpr int NTQ = DVQ / 32;                // 32-column output tiles per wave
+    static constexpr int QC = DK / 4;                   // 16-byte f32 chunks per q row
+    static constexpr int QD = HG * QC / 64 / NWAVE;     // q DMA instructions per wave
+    static constexpr int PROW = TK + 8;                 // P exchange row pitch (halves)
+    static constexpr int OREG = DVQ * HG * 2;           // a wave's f16 [DVQ][32 heads] output region
+    static constexpr int OPT = HG * DVQ / 8 / 64;       // 16-byte output chunks per lane
+    static_assert(QC % 16 == 0 && (HG * QC) % (64 * NWAVE) == 0, "q staging swizzle, whole q DMA instructions");
+    static_assert(HG * DK * 4 <= NWAVE * STAGE, "the f32 q staging fits stage 1 of the ring");
+    static_assert(NWAVE * OREG <= RING, "the output regions fit the ring");
+    static_assert((NWAVE - 1) * STAGE + 1024 * NTQ < 65536, "P.V operand offsets fit the DS immediate");
 };
+
+// Stage layout (one wave slice, 16 cache rows): 1 KB blocks i = 0 .. CH/4 - 1, block i holding chunks
+// 4 i .. 4 i + 3 (16 bytes each) of the 16 rows, chunk 4 i + q of row r at slot 16 q + (r ^ 4 q).
+// DMA instruction i fills block i, lane l fetching row (l & 15) ^ 4 (l >> 4), chunk 4 i + (l >> 4),
+// so its global offset is lane-only plus 64 i.  The XOR keeps the Q.K^T reads (16 rows, one chunk)
+// and the transpose reads (4 rows x 4 chunks per 32 lanes) on distinct banks, at 128 or 256 bytes
+// per LDS clock alike.
+__device__ __forceinline__ int slot_of(int r, int q) { return 16 * q + (r ^ (4 * q)); }
+
+// Unit swizzle of the output regions ([DVQ rows][32 heads] f16, rows of 8 8-byte units): unit u of
+// row dv sits at slot u ^ ounit(dv), ounit = 4 b1 ^ b2 ^ 6 b3 ^ 2 b4 (b_i = bit i of dv).  The
+// stores (32 consecutive rows, one unit) and the transpose reads (4 rows x 4 units per 16 lanes,
+// rows 8 apart across 16-lane pairs) then hit distinct banks at 128 or 256 bytes per LDS clock.
+__device__ __forceinline__ int ounit(int dv) {
+    return (((dv >> 1) & 1) << 2) ^ ((dv >> 2) & 1) ^ (((dv >> 3) & 1) * 6) ^ (((dv >> 4) & 1) << 1);
+}
 
 template <int DK, int DV>
 __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) {
     using C = DecodeCfg<DK, DV>;
-    __shared__ __attribute__((aligned(16))) half_t kt[TK * C::KROW];     // the current tile; the output block at the end
-    __shared__ __attribute__((aligned(16))) half_t qs[HG * C::KROW];     // f16 q block [32 heads][DK] (prologue)
-    __shared__ __attribute__((aligned(16))) half_t pl[HG * C::PROW];     // P [32 heads][64 keys]
-    __shared__ __attribute__((aligned(16))) f32x4 sx[NWAVE][2][64];      // half-score exchange
-    __shared__ __attribute__((aligned(16))) float mk[TK];              // the tile's mask values
-    __shared__ float red_max[2][HG];
-    __shared__ float red_sum[2][HG];
-    __shared__ __attribute__((aligned(16))) float alpha_s[HG];
-    __shared__ float l_fin[HG];
+    __shared__ __attribute__((aligned(16))) char ring[C::RING];          // [stage][wave] K rows + mask
+    __shared__ __attribute__((aligned(16))) half_t px[2][HG * C::PROW];  // P exchange, by tile parity
+    __shared__ __attribute__((aligned(16))) float red[2][NWAVE][HG];     // slice maxima, by tile parity
+    __shared__ float fin_t[NWAVE][HG];
+    __shared__ float fin_l[NWAVE][HG];
+    __shared__ float fin_r[HG];
+    __shared__ __attribute__((aligned(16))) float inv_l[HG];
+    __shared__ float hdr[2 * HG];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sp = blockIdx.x;
     const int hg0 = blockIdx.y * HG;
     const int t = blockIdx.z;
+    const int g = lane >> 4;                 // 16-lane group
+    const int j16 = lane & 15;
 
-    // ---- split range (balanced partition of whole tiles) ----
+    // ---- split range (balanced partition of whole 64-key tiles) ----
     const int base_t = a.n_tiles / a.n_split;
     const int rem = a.n_tiles % a.n_split;
     const int t0 = sp * base_t + min(sp, rem);
-    const int t1 = t0 + base_t + (sp < rem ? 1 : 0);
+    const int n_my = base_t + (sp < rem ? 1 : 0);
 
-    const int kg = w & 1;                          // keys [32 kg, 32 kg + 32) of the tile
-    const int dh = w >> 1;                         // QK: D_k half; softmax: head tile
-    const int kl0 = 32 * kg + 4 * (lane >> 4);     // lane's score keys: kl0 + 16 m + r (m < 2, r < 4)
-    const int hl = 16 * dh + (lane & 15);          // this lane's score head (workgroup-local)
-    // no branch may guard a tile load: the compiler's wait counts are exact only when every path
-    // issues the same loads, so a missing mask reads q's (valid) memory and is zeroed after the load
     const bool has_mask = a.mask != nullptr;
     const float * mrow = has_mask ? reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) + (size_t)t * a.mask_nb1) : a.q;
-    const int n_my = t1 - t0;                                   // tiles of this split
-    auto tile_of = [&](int j) { return min(t0 + min(j, n_my - 1), a.n_tiles - 1); };   // clamped, always valid
 
-    // ---- 1. q block of this workgroup (32 heads x DK f32): one coalesced pass, issued first ----
-    f32x4 qv[C::QPT];
-#pragma unroll
-    for (int i = 0; i < C::QPT; ++i) {
-        const int c = i * NTHR + tid;
-        const int hh = c / (DK / 4);
-        const int d4 = c - hh * (DK / 4);
-        const int h = min(hg0 + hh, a.n_head - 1);
-        const f32x4 x = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(a.q) + (size_t)t * a.q_nb2 +
-                                                       (size_t)h * a.q_nb1 + (size_t)d4 * 16);
-        qv[i] = (hg0 + hh < a.n_head) ? x : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    // ---- 2. tile staging: a register double buffer A/B ----
-    const uint32_t nb1 = (uint32_t)a.kc_nb1;
-    // one mask value per key of the tile rides with the tile (thread t loads key t & 63; it is
-    // staged through LDS at commit), so each tile is exactly NPT + 1 loads per thread
-    u32x4 stgA[C::NPT], stgB[C::NPT];
-    float mskA, mskB;
-    auto issue = [&](u32x4 (&stg)[C::NPT], float & msk, int tile) {
-        const char * tb = a.kc + (size_t)tile * TK * a.kc_nb1;     // wave-uniform tile base
-        const int nk = min(TK, a.n_kv - tile * TK);
-        const float mv = mrow[(size_t)(has_mask ? tile * TK : 0) + min(tid & (TK - 1), nk - 1)];
-        msk = has_mask ? mv : 0.0f;
-#pragma unroll
-        for (int i = 0; i < C::NPT; ++i) {
-            const int c = i * NTHR + tid;
-            const int key = c / C::CH;
-            const int cc = c - key * C::CH;
-            stg[i] = ld16_stream(tb + (uint32_t)min(key, nk - 1) * nb1 + (uint32_t)cc * 16u);
-        }
+    // ---- DMA of this wave's 16-key slice of tile k into stage s: DMA_N + 1 loads ----
+    // The resources are rebased on the slice, num_records = bytes up to the end of row n_kv - 1,
+    // so rows (and mask entries) at or past n_kv are returned as zeros by the range check.
+    const uint32_t ring_lds = lds_addr(ring);
+    auto stage_off = [&](int s, int v) { return (s * NWAVE + v) * C::STAGE; };
+    const uint32_t kvoff = (uint32_t)(((lane & 15) ^ (4 * (lane >> 4))) * a.kc_nb1) + 16u * (uint32_t)(lane >> 4);
+    const uint32_t mvoff = 4u * (uint32_t)j16;
+    struct SliceDma { i32x4 krs, mrs; uint32_t sb; };
+    auto plan = [&](int s, int k) {
+        const int tile = min(t0 + min(k, n_my - 1), a.n_tiles - 1);
+        const int key0 = tile * TK + WK * w;
+        const int left = a.n_kv - key0;                  // rows of this slice that exist (may be <= 0)
+        SliceDma d;
+        d.krs = make_rsrc(a.kc + (int64_t)key0 * a.kc_nb1, left > 0 ? (uint32_t)((int64_t)(left - 1) * a.kc_nb1 + DK * 2) : 0u);
+        d.mrs = make_rsrc(mrow + key0, (has_mask && left > 0) ? (uint32_t)left * 4u : 0u);
+        d.sb = ring_lds + (uint32_t)stage_off(s, w);
+        return d;
     };
-    // Tile A goes in flight behind q; tile B only after q has been consumed, so that no wait below
-    // ever needs more than the hardware's 63 outstanding vector-memory operations (beyond that the
-    // compiler's conservative count makes the q conversion wait for both tiles).
-    issue(stgA, mskA, tile_of(0));
+    // instruction i < DMA_N: block i of the rows; i == DMA_N: the mask slot (float l = key key0 + (l & 15))
+    auto put = [&](const SliceDma & d, int i) {
+        if (i < C::DMA_N) dma16_nt(d.krs, kvoff, (uint32_t)(64 * i), d.sb + (uint32_t)(1024 * i));
+        else dma4(d.mrs, mvoff, 0u, d.sb + (uint32_t)C::ROWS_BYTES);
+    };
 
-    // ---- 3. q -> f16 via LDS -> this wave's B fragments: 32 heads x its D_k half ----
+    // ---- q block (32 heads x DK f32) -> stage 1 by DMA, then f16 B fragments in registers ----
+    // Staging slot of f32 chunk c (4 floats) of head h: h * QC + (c ^ (h & 15)), so the fragment
+    // reads below (16 heads, one chunk) hit distinct banks.  The q DMA goes first and tile 0
+    // streams behind it; heads past n_head read as zeros.
+    {
+        const int nh = min(HG, a.n_head - hg0);
+        const i32x4 qrs = make_rsrc(reinterpret_cast<const char *>(a.q) + (size_t)t * a.q_nb2 + (size_t)hg0 * a.q_nb1,
+                                    (uint32_t)((int64_t)(nh - 1) * a.q_nb1 + DK * 4));
+        const uint32_t qsb = ring_lds + (uint32_t)(NWAVE * C::STAGE);
 #pragma unroll
-    for (int i = 0; i < C::QPT; ++i) {
-        const int c = i * NTHR + tid;
-        const int hh = c / (DK / 4);
-        const int d4 = c - hh * (DK / 4);
-        half4 h4;
-        h4[0] = to_half(qv[i][0]); h4[1] = to_half(qv[i][1]); h4[2] = to_half(qv[i][2]); h4[3] = to_half(qv[i][3]);
-        *reinterpret_cast<half4 *>(&qs[hh * C::KROW + 4 * d4]) = h4;
+        for (int i = 0; i < C::QD; ++i) {
+            const int p = (w * C::QD + i) * 64 + lane;
+            const int h = p / C::QC;
+            const int c = (p - h * C::QC) ^ (h & 15);
+            dma16(qrs, (uint32_t)(h * a.q_nb1) + 16u * (uint32_t)c, 0u, qsb + (uint32_t)((w * C::QD + i) * 1024));
+        }
+        const SliceDma d0 = plan(0, 0);
+#pragma unroll
+        for (int i = 0; i <= C::DMA_N; ++i) put(d0, i);
     }
+    wait_vm<C::DMA_N + 1>();                 // this wave's part of q has landed
     __syncthreads();
-    half8 qreg[2][C::HSTEPS];  // [head tile][step]: head 16 n + (lane & 15), d = 32 (HSTEPS dh + s) + 8 (lane >> 4) .. +7
+    half8 qreg[2][C::QSTEPS];   // [head tile n][step s]: head 16 n + j16, d = 32 s + 8 g .. +7
+    {
+        const float * qs = reinterpret_cast<const float *>(ring + NWAVE * C::STAGE);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-        const half_t * qr = &qs[(16 * n + (lane & 15)) * C::KROW + 32 * C::HSTEPS * dh + 8 * (lane >> 4)];
+        for (int n = 0; n < 2; ++n)
 #pragma unroll
-        for (int s = 0; s < C::HSTEPS; ++s) qreg[n][s] = *reinterpret_cast<const half8 *>(qr + 32 * s);
+            for (int s = 0; s < C::QSTEPS; ++s) {
+                const float * row = qs + 4 * (16 * n + j16) * C::QC;
+                const f32x4 x0 = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * s + 2 * g) ^ j16));
+                const f32x4 x1 = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * s + 2 * g + 1) ^ j16));
+                qreg[n][s] = half8{to_half(x0[0]), to_half(x0[1]), to_half(x0[2]), to_half(x0[3]),
+                                   to_half(x1[0]), to_half(x1[1]), to_half(x1[2]), to_half(x1[3])};
+            }
     }
-    issue(stgB, mskB, tile_of(1));
+    __syncthreads();                         // the q staging in stage 1 is free again
 
-    // ---- running state: lane tracks head hl (replicated across the 2 key-group waves) ----
-    float m_run = -INFINITY;   // log2 units
-    float l_run = 0.0f;
-    f32x16 o[C::NT_DV];
+    // ---- running state: reference max identical in every wave; l and exact max of own keys ----
+    float m_ref[2] = {-INFINITY, -INFINITY}; // heads 16 n + j16, log2 units
+    float m_top[2] = {-INFINITY, -INFINITY};
+    float l_part[2] = {0.0f, 0.0f};
+    f32x16 o[C::NTQ];                        // tile i: C row = head, C col = column DVQ w + 32 i + (lane & 31)
 #pragma unroll
-    for (int i = 0; i < C::NT_DV; ++i)
+    for (int i = 0; i < C::NTQ; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
 
-    auto compute = [&](u32x4 (&stg)[C::NPT], float & msk, int tile, bool refill) {
-        __syncthreads();                                  // (A) previous tile's LDS reads done
-#pragma unroll
-        for (int i = 0; i < C::NPT; ++i) {
-            const int c = i * NTHR + tid;
-            const int key = c / C::CH;
-            const int cc = c - key * C::CH;
-            *reinterpret_cast<u32x4 *>(&kt[key * C::KROW + cc * 8]) = stg[i];
-        }
-        if (tid < TK) mk[tid] = msk;
-        if (refill) issue(stg, msk, tile_of(tile - t0 + 2));   // refill this buffer two tiles ahead
-        __syncthreads();                                  // (B) tile in LDS
+    // P.V operand addresses: A = P rows (lane & 31), keys 16 ks + 8 (lane >> 5); B = two transpose
+    // reads per tile, in 16-lane group g lane j supplying row 8 (g >> 1) + (j >> 2) (then + 4) of key
+    // slice ks, 4 columns at DVQ w + 32 i + 16 (g & 1) + 4 (j & 3)
+    const int pv_r0 = 8 * (g >> 1) + (j16 >> 2);
+    const int pv_cq = 2 * (g & 1) + ((j16 & 3) >> 1);
+    const int pv_lo = 16 * slot_of(pv_r0, pv_cq) + 8 * (j16 & 1) + 1024 * (C::NTQ * w);
+    const int pv_hi = 16 * slot_of(pv_r0 + 4, pv_cq) + 8 * (j16 & 1) + 1024 * (C::NTQ * w);
 
-        // half-scores: 32 keys (two 16-key M tiles) x 32 heads over this wave's D_k half; each
-        // K chunk is read from LDS once and feeds both head tiles
-        f32x4 acc[2][2];
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-#pragma unroll
-            for (int n = 0; n < 2; ++n) acc[m][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const half_t * arow = &kt[(32 * kg + 16 * m + (lane & 15)) * C::KROW + 32 * C::HSTEPS * dh + 8 * (lane >> 4)];
-#pragma unroll
-            for (int s = 0; s < C::HSTEPS; ++s) {
-                const half8 av = *reinterpret_cast<const half8 *>(arow + 32 * s);
-                acc[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc[m][0], 0, 0, 0);
-                acc[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc[m][1], 0, 0, 0);
-            }
-        }
-        // give the partner wave (same keys, other D_k half) the head tile it owns; keep ours
-#pragma unroll
-        for (int m = 0; m < 2; ++m) sx[w][m][lane] = dh ? acc[m][0] : acc[m][1];
-        __syncthreads();                                  // (B2)
+    for (int k = 0; k < n_my; ++k) {
+        wait_vm<0>();                        // this wave's slice of tile k has landed
+        // every wave is past P.V of tile k - 1, so stage (k + 1) & 1 can take tile k + 1: its DMA
+        // is spread over this tile's Q.K^T steps, which the memory stream then paces
+        if (k >= 1) __syncthreads();
+        const bool pf = k + 1 < n_my;
+        const SliceDma dn = plan((k + 1) & 1, k + 1);
+        const int par = k & 1;
+        const char * sb = ring + stage_off(par, w);
+        const int kbase = (t0 + k) * TK + WK * w;
 
-        const int kbase = tile * TK;
-        float sc[8];
-        float lmax = -INFINITY;
+        // S^T = K . Q^T : the wave's 16 keys (C rows) x 32 heads (C cols, two 16-wide tiles)
+        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+        {
+            // operand reads run QPF steps ahead of the MFMAs that consume them; the scheduling
+            // barriers keep the compiler from sinking them back next to their use
+            constexpr int QPF = 4;
+            const char * abase = sb + 16 * slot_of(j16, g);     // row j16, chunk 4 s + g of block s
+            half8 abuf[QPF];
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const f32x4 full = (dh ? acc[m][1] : acc[m][0]) + sx[w ^ 2][m][lane];
-            const f32x4 mv = *reinterpret_cast<const f32x4 *>(&mk[kl0 + 16 * m]);
+            for (int s = 0; s < QPF; ++s) abuf[s] = *reinterpret_cast<const half8 *>(abase + 1024 * s);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = full[r] * a.scale_log2 + mv[r] * LOG2E;
-                sc[4 * m + r] = (kbase + kl0 + 16 * m + r < a.n_kv) ? v : -INFINITY;
-                lmax = fmaxf(lmax, sc[4 * m + r]);
+            for (int s = 0; s < C::QSTEPS; ++s) {
+                const half8 av = abuf[s % QPF];
+                if (s + QPF < C::QSTEPS) abuf[s % QPF] = *reinterpret_cast<const half8 *>(abase + 1024 * (s + QPF));
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc1, 0, 0, 0);
+                if (pf && s <= C::DMA_N) put(dn, s);
+                __builtin_amdgcn_sched_barrier(0);
             }
+#pragma unroll
+            for (int i = C::QSTEPS; i <= C::DMA_N; ++i)
+                if (pf) put(dn, i);
         }
-        lmax = fmaxf(lmax, shfl_xor(lmax, 16));
-        lmax = fmaxf(lmax, shfl_xor(lmax, 32));
-        if (lane < 16) red_max[kg][hl] = lmax;
-        __syncthreads();                                  // (C)
-
-        const float tmax = fmaxf(red_max[0][hl], red_max[1][hl]);
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = (m_run == -INFINITY) ? 0.0f : exp2_fast(m_run - m_new);
-        float psum = 0.0f;
+        // scores (log2 units) of keys 4 g + r for heads j16 (n = 0) and 16 + j16 (n = 1)
+        const f32x4 mk = *reinterpret_cast<const f32x4 *>(sb + C::ROWS_BYTES + 16 * g);
+        float sc[2][4];
+        float mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            half4 ph;
+        for (int r = 0; r < 4; ++r) {
+            const bool live = kbase + 4 * g + r < a.n_kv;
+            const float mb = mk[r] * LOG2E;              // zeros when there is no mask
+            sc[0][r] = live ? acc0[r] * a.scale_log2 + mb : -INFINITY;
+            sc[1][r] = live ? acc1[r] * a.scale_log2 + mb : -INFINITY;
+            mx[0] = fmaxf(mx[0], sc[0][r]);
+            mx[1] = fmaxf(mx[1], sc[1][r]);
+        }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float x = sc[4 * m + r];
-                const float p = (x == -INFINITY) ? 0.0f : exp2_fast(x - m_new);
-                psum += p;
-                ph[r] = to_half(p);
+        for (int n = 0; n < 2; ++n) {
+            mx[n] = fmaxf(mx[n], shfl_xor(mx[n], 16));
+            mx[n] = fmaxf(mx[n], shfl_xor(mx[n], 32));
+            m_top[n] = fmaxf(m_top[n], mx[n]);
+        }
+        // P against the current reference (exact unless the reference moves below; the clamp only
+        // keeps a provisional value finite), into the exchange as [32 heads][64 keys]
+        half_t * pxv = px[par];
+        float p[2][4];
+        auto put_p = [&]() {
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                half4 ph;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    p[n][r] = (sc[n][r] == -INFINITY) ? 0.0f : exp2_fast(fminf(sc[n][r] - m_ref[n], 15.0f));
+                    ph[r] = to_half(p[n][r]);
+                }
+                *reinterpret_cast<half4 *>(&pxv[(16 * n + j16) * C::PROW + WK * w + 4 * g]) = ph;
             }
-            *reinterpret_cast<half4 *>(&pl[hl * C::PROW + kl0 + 16 * m]) = ph;
-        }
-        psum += shfl_xor(psum, 16);
-        psum += shfl_xor(psum, 32);
+        };
+        put_p();
         if (lane < 16) {
-            red_sum[kg][hl] = psum;
-            if (kg == 0) alpha_s[hl] = alpha;
+            red[par][w][lane] = mx[0];
+            red[par][w][16 + lane] = mx[1];
         }
-        m_run = m_new;
-        __syncthreads();                                  // (D)
-
-        l_run = alpha * l_run + (red_sum[0][hl] + red_sum[1][hl]);
-
-        // O[32 heads x DVW] = alpha * O + P . V ; lane's C rows: heads 8 (r/4) + 4 (lane>>5) + (r&3)
+        __syncthreads();
+        // the tile's max per head; every wave reads the same values and holds the same reference,
+        // so the decision below is uniform over the workgroup
+        bool move = false;
+        float tm[2];
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const float4 al = *reinterpret_cast<const float4 *>(&alpha_s[8 * q4 + 4 * (lane >> 5)]);
+        for (int n = 0; n < 2; ++n) {
+            tm[n] = fmaxf(fmaxf(red[par][0][16 * n + j16], red[par][1][16 * n + j16]),
+                          fmaxf(red[par][2][16 * n + j16], red[par][3][16 * n + j16]));
+            move |= (m_ref[n] == -INFINITY) ? (tm[n] != -INFINITY) : (tm[n] > m_ref[n] + LAZY);
+        }
+        if (__builtin_amdgcn_ballot_w64(move) != 0) {     // rare: move the reference, rescale, redo P
+            float al[2];
 #pragma unroll
-            for (int i = 0; i < C::NT_DV; ++i) {
-                o[i][4 * q4 + 0] *= al.x;
-                o[i][4 * q4 + 1] *= al.y;
-                o[i][4 * q4 + 2] *= al.z;
-                o[i][4 * q4 + 3] *= al.w;
+            for (int n = 0; n < 2; ++n) {
+                const bool mv = (m_ref[n] == -INFINITY) ? (tm[n] != -INFINITY) : (tm[n] > m_ref[n] + LAZY);
+                al[n] = !mv ? 1.0f : (m_ref[n] == -INFINITY ? 0.0f : exp2_fast(m_ref[n] - tm[n]));
+                m_ref[n] = mv ? tm[n] : m_ref[n];
+                l_part[n] *= al[n];
             }
-        }
-        // B = V[keys][cols] straight from the row-major tile with the gfx950 transpose read: in each
-        // 16-lane group, lane j supplies row (j >> 2), columns 4 (j & 3) .. +3 of a 4 x 16 block and
-        // receives column j of it; two reads give the lane its 8 consecutive keys.
-        const half_t * vbase = &kt[(8 * (lane >> 5) + ((lane & 15) >> 2)) * C::KROW + w * C::DVW +
-                                   16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
-#pragma unroll 1
-        for (int kk = 0; kk < TK / 16; ++kk) {           // not unrolled: bounds the live operand registers
-            const half8 pa = *reinterpret_cast<const half8 *>(&pl[(lane & 31) * C::PROW + 16 * kk + 8 * (lane >> 5)]);
+            // accumulator rows are heads 8 (r / 4) + 4 (lane >> 5) + (r & 3): fetch their factors
+            // from the lanes holding them (head h's factor sits in lane h & 15 of set n = h >> 4)
+            f32x16 al16;
 #pragma unroll
-            for (int i = 0; i < C::NT_DV; ++i) {
-                const half_t * vp = vbase + 16 * kk * C::KROW + 32 * i;
-                const half4 lo = lds_read_tr16(vp);
-                const half4 hi = lds_read_tr16(vp + 4 * C::KROW);
+            for (int r = 0; r < 16; ++r) {
+                const int h = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const float a0 = __shfl(al[0], h & 15, 64), a1 = __shfl(al[1], h & 15, 64);
+                al16[r] = (h >> 4) ? a1 : a0;
+            }
+            // In place on the accumulator registers, one asm block per element, so that they stay
+            // in AGPRs across this branch (a plain multiply makes the register allocator move the
+            // tile set through VGPRs).  The s_nops cover the MFMA -> VALU read distance.
+            if (k > 0) {                          // (on the first tile the accumulators are still 0)
+                asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+                for (int i = 0; i < C::NTQ; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        float tmp;
+                        asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                                     : "+a"(o[i][r]), "=&v"(tmp) : "v"(al16[r]));
+                    }
+                asm volatile("s_nop 7" ::: "memory");
+            }
+            put_p();
+            __syncthreads();
+        }
+#pragma unroll
+        for (int n = 0; n < 2; ++n) l_part[n] += (p[n][0] + p[n][1]) + (p[n][2] + p[n][3]);
+
+        // O[:, own columns] += P . V over the tile's 64 keys (4 slices x 16)
+#pragma unroll
+        for (int ks = 0; ks < NWAVE; ++ks) {
+            const half8 pa = *reinterpret_cast<const half8 *>(&pxv[(lane & 31) * C::PROW + WK * ks + 8 * (lane >> 5)]);
+            const char * vs = ring + stage_off(par, ks);
+#pragma unroll
+            for (int i = 0; i < C::NTQ; ++i) {
+                const half4 lo = lds_read_tr16(reinterpret_cast<const half_t *>(vs + pv_lo + 1024 * i));
+                const half4 hi = lds_read_tr16(reinterpret_cast<const half_t *>(vs + pv_hi + 1024 * i));
                 const half8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, vb, o[i], 0, 0, 0);
             }
         }
-    };
-
-    // steady state: both refills are unconditional (an odd tile count loads one tile twice); the
-    // last two tiles are peeled and issue nothing
-    int j = 0;
-    for (; j + 2 < n_my; j += 2) {
-        compute(stgA, mskA, t0 + j, true);
-        compute(stgB, mskB, t0 + j + 1, true);
     }
-    if (j < n_my) compute(stgA, mskA, t0 + j, false);
-    if (j + 1 < n_my) compute(stgB, mskB, t0 + j + 1, false);
+    wait_vm<0>();                            // nothing of this wave may still target the ring
 
-    // ---- epilogue: o / l per head -> f16 block in LDS -> 16-byte stores ----
-    if (kg == 0 && lane < 16) l_fin[hl] = l_run;
-    __syncthreads();                                      // last tile's LDS reads done; l_fin visible
+    // thread indices re-derived through an opaque move, so that the epilogue's address arithmetic
+    // is computed here rather than before the loop and kept alive (or spilled) across it
+    int tid_e;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"(tid));
+    const int lane_e = tid_e & 63;
+
+    // ---- per head: M = exact max over the waves, L = sum of the waves' l (common reference) ----
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        l_part[n] += shfl_xor(l_part[n], 16);
+        l_part[n] += shfl_xor(l_part[n], 32);
+    }
+    if (lane_e < 16) {
+        fin_t[w][lane_e] = m_top[0];
+        fin_t[w][16 + lane_e] = m_top[1];
+        fin_l[w][lane_e] = l_part[0];
+        fin_l[w][16 + lane_e] = l_part[1];
+        if (w == 0) {
+            fin_r[lane_e] = m_ref[0];
+            fin_r[16 + lane_e] = m_ref[1];
+        }
+    }
+    __syncthreads();
+    if (tid_e < HG) {
+        float M = -INFINITY, L = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NWAVE; ++v) {
+            M = fmaxf(M, fin_t[v][tid_e]);
+            L += fin_l[v][tid_e];
+        }
+        inv_l[tid_e] = L > 0.0f ? 1.0f / L : 0.0f;
+        hdr[tid_e] = (M == -INFINITY) ? -INFINITY : M * LN2;                        // natural-log units
+        hdr[HG + tid_e] = L > 0.0f ? L * exp2_fast(fin_r[tid_e] - M) : 0.0f;       // relative to M
+    }
+    __syncthreads();
+
     const bool direct = a.dst != nullptr;                 // single split: final f32 output to dst
-    char * blk = direct ? nullptr : a.part + (((size_t)blockIdx.y * a.nt + t) * a.n_split + sp) * part_block_bytes(DV, 2);
-    if (!direct && kg == 0 && lane < 16) {
-        float * hdr = reinterpret_cast<float *>(blk);
-        hdr[hl] = (m_run == -INFINITY) ? -INFINITY : m_run * LN2;
-        hdr[PART_HEADS + hl] = l_run;
-    }
-    half_t * ob = kt;                                     // [HG][DV] f16
+    if (direct) {
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const f32x4 s4 = *reinterpret_cast<const f32x4 *>(&inv_l[8 * q4 + 4 * (lane_e >> 5)]);
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-            const int hloc = 8 * q4 + 4 * (lane >> 5) + r4;
-            const float l = l_fin[hloc];
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            const int dv = w * C::DVW + (lane & 31);
-            if (direct) {
-                if (hg0 + hloc < a.n_head) {
-                    float * drow = a.dst + ((size_t)(hg0 + hloc) * a.nt + t) * DV + dv;
+            for (int e = 0; e < 4; ++e) {
+                const int h = hg0 + 8 * q4 + 4 * (lane_e >> 5) + e;
+                if (h < a.n_head) {
+                    float * d = a.dst + ((size_t)h * a.nt + t) * DV + C::DVQ * w + (lane_e & 31);
 #pragma unroll
-                    for (int i = 0; i < C::NT_DV; ++i) drow[32 * i] = o[i][4 * q4 + r4] * inv;
+                    for (int i = 0; i < C::NTQ; ++i) d[32 * i] = o[i][4 * q4 + e] * s4[e];
                 }
-            } else {
-#pragma unroll
-                for (int i = 0; i < C::NT_DV; ++i) ob[hloc * DV + dv + 32 * i] = to_half(o[i][4 * q4 + r4] * inv);
             }
         }
-    if (direct) return;
-    __syncthreads();
+        return;
+    }
+    // o / l in f16 into this wave's region of the (idle) ring, [DVQ rows][32 heads], then read back
+    // transposed into [32 heads][D_v] chunks of 8 columns
+    char * reg = ring + w * C::OREG;
+    {
+        const int dvl = lane_e & 31, hi32 = lane_e >> 5;
 #pragma unroll
-    for (int i = 0; i < C::OPT; ++i) {
-        const int c = i * NTHR + tid;                     // 16-byte chunk of the [HG][DV] f16 block
-        if (hg0 + c / (DV / 8) < a.n_head)
-            *reinterpret_cast<u32x4 *>(blk + 256 + (size_t)c * 16) = *reinterpret_cast<const u32x4 *>(&ob[c * 8]);
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const f32x4 s4 = *reinterpret_cast<const f32x4 *>(&inv_l[8 * q4 + 4 * hi32]);
+#pragma unroll
+            for (int i = 0; i < C::NTQ; ++i) {
+                const int dv = 32 * i + dvl;
+                half4 hv;
+                hv[0] = to_half(o[i][4 * q4 + 0] * s4[0]);
+                hv[1] = to_half(o[i][4 * q4 + 1] * s4[1]);
+                hv[2] = to_half(o[i][4 * q4 + 2] * s4[2]);
+                hv[3] = to_half(o[i][4 * q4 + 3] * s4[3]);
+                *reinterpret_cast<half4 *>(reg + dv * 64 + 8 * ((2 * q4 + hi32) ^ ounit(dv))) = hv;
+            }
+        }
+    }
+    __syncthreads();
+    char * blk = a.part + (((size_t)blockIdx.y * a.nt + t) * a.n_split + sp) * part_block_bytes(DV, 2);
+    if (tid_e < 2 * HG) reinterpret_cast<float *>(blk)[tid_e] = hdr[tid_e];
+    // per 64-chunk group cg: heads 16 hb + (lane & 15), columns 8 (4 (cg >> 1) + (lane >> 4)) .. +7
+    const int ge = lane_e >> 4, je = lane_e & 15;
+#pragma unroll
+    for (int cg = 0; cg < C::OPT; ++cg) {
+        const int hb = cg & 1;
+        const int dv8 = 4 * (cg >> 1) + ge;
+        const int dv_lo = 8 * dv8 + (je >> 2), dv_hi = dv_lo + 4;
+        const int u = 4 * hb + (je & 3);
+        const half4 lo = lds_read_tr16(reinterpret_cast<const half_t *>(reg + dv_lo * 64 + 8 * (u ^ ounit(dv_lo))));
+        const half4 hi = lds_read_tr16(reinterpret_cast<const half_t *>(reg + dv_hi * 64 + 8 * (u ^ ounit(dv_hi))));
+        const half8 hv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<half8 *>(blk + 256 + ((size_t)(16 * hb + je) * DV + C::DVQ * w + 8 * dv8) * 2) = hv;
     }
 }
 

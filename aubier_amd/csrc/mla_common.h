@@ -48,6 +48,40 @@ __device__ __forceinline__ half4 lds_read_tr16(const half_t * p) {
     return __builtin_bit_cast(half4, v);
 }
 
+// LDS DMA through a raw buffer resource (gfx950 buffer_load_dword{,x4} ... lds).  Lane l's 4 (or
+// 16) bytes at rsrc.base + voff + soff land in LDS at lds_base + l * 4 (or * 16); lds_base is
+// wave-uniform (it goes through M0).  The hardware range check of the resource makes a read at
+// or past num_records return zeros, so tails need no clamping.  Issued from inline asm so that
+// the compiler does not track them (its conservative handling of LDS DMA would wait for every DMA
+// in flight before any LDS read): the caller owns the waits (s_waitcnt vmcnt).
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 make_rsrc(const void * base, uint32_t num_records) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    i32x4 r;
+    r[0] = (int32_t)(uint32_t)b;
+    r[1] = (int32_t)((uint32_t)(b >> 32) & 0xffffu);     // stride 0
+    r[2] = (int32_t)num_records;
+    r[3] = 0x00020000;                                  // gfx9 dword 3: DATA_FORMAT 32
+    return r;
+}
+__device__ __forceinline__ uint32_t lds_addr(const void * p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_base) : "memory");
+}
+// the same with the non-temporal policy: for data read once (a streamed cache), so that it does
+// not displace reused data from the caches
+__device__ __forceinline__ void dma16_nt(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds" :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ void dma4(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" :: "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_base) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // 16-byte global load/store helpers
 __device__ __forceinline__ u32x4 ld16(const void * p) { return *reinterpret_cast<const u32x4 *>(p); }
 __device__ __forceinline__ u32x4 ld16_stream(const void * p) {

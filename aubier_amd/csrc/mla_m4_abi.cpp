@@ -40,6 +40,7 @@ bool is_contiguous(const mla_m4_tensor * t) {
 // ---------------------------------------------------------------- KQKV contract
 struct KqkvShape {
     int64_t dk, dv, n_kv, n_head, nt;
+    int64_t kc_nb1;
     int32_t kc_type;
     bool has_mask;
 };
@@ -78,13 +79,18 @@ int check_kqkv(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_t
     s->n_kv = kc->ne[1];
     s->n_head = q->ne[1];
     s->nt = q->ne[2];
+    s->kc_nb1 = (int64_t)kc->nb[1];
     s->kc_type = kc->type;
     s->has_mask = has_mask;
     return MLA_M4_OK;
 }
 
+// The MFMA kernel addresses the cache through a buffer resource with 32-bit byte offsets, so the
+// rows it reads must end within 4 GiB of the cache base (n_kv <= 3.7M keys of a 576-wide f16
+// cache); larger caches take the generic kernel.
 bool use_mfma(const KqkvShape & s) {
-    return s.kc_type == MLA_M4_TYPE_F16 && mla::decode_f16_supported((int)s.dk, (int)s.dv);
+    const uint64_t span = (uint64_t)(s.n_kv - 1) * (uint64_t)s.kc_nb1 + (uint64_t)s.dk * 2u;
+    return s.kc_type == MLA_M4_TYPE_F16 && mla::decode_f16_supported((int)s.dk, (int)s.dv) && span <= 0xFFFFFFFFull;
 }
 
 int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
