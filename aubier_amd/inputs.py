@@ -5,7 +5,7 @@ Values are N(0,1)*0.05 from splitmix64 + Box-Muller, so they are identical on ev
 Value i of a stream depends only on (seed, i): pair p = i // 2 seeds its own splitmix64 state
 with seed ^ (0xD1B54A32D192ED03 * (p + 1)) and draws two uniforms u1, u2 in (0, 1];
 z0 = sqrt(-2 ln u1) cos(2 pi u2), z1 = sqrt(-2 ln u1) sin(2 pi u2), computed in double and rounded
-once to f32 after scaling.  An f16 cache is cast with round-to-nearest-even after scaling.
+once to f32 after scaling by the f32 scale.  An f16 cache is cast with round-to-nearest-even after scaling.
 
 Geometry (all configs): 32 heads, q = 128 nope + 64 rope per head, KV row = 512 latent + 64 rope,
 W_kb [H][D_v][d_n] = ggml ne [128, 512, 32] f32, kq_scale = 1/sqrt(192), mask 0 / -inf.
@@ -40,6 +40,7 @@ def _mix(z: np.ndarray) -> np.ndarray:
 def randn(seed: int, n: int, scale: float = 0.05) -> np.ndarray:
     """n f32 values N(0,1)*scale from the counter-based splitmix64/Box-Muller stream `seed`."""
     npairs = (n + 1) // 2
+    scale = float(np.float32(scale))     # the scale is an f32 parameter (as in the C generator)
     out = np.empty(2 * npairs, dtype=np.float32)
     chunk = 1 << 22
     with np.errstate(over="ignore"):

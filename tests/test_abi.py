@@ -1,0 +1,144 @@
+"""CPU tests of the C ABI (include/mla_m4.h, aubier_amd/libmla_m4.so): the library loads, exports
+every entry point the header declares, and its host-side contract checks (the supports_op
+mirrors, status codes, the tri-state flag, split counts) behave as documented.  No kernel is
+launched: every call here either only inspects descriptors or is rejected before any launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import aubier_amd as A
+from aubier_amd import ops
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mla_m4.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return A.load_library()
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mla_m4_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_are_all_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    # and the Python mirror binds exactly the declared set
+    assert sorted(ops.exported_symbols()) == names
+
+
+def test_version_and_status_strings(lib):
+    assert lib.mla_m4_version().decode().startswith("mla-m4-gfx950")
+    for code, text in ops.STATUS.items():
+        assert lib.mla_m4_status_str(code).decode() == text
+    assert lib.mla_m4_status_str(-99).decode() == "unknown status"
+
+
+@pytest.mark.parametrize("flag,gpu,want", [(-1, 1, 1), (-1, 0, 0), (0, 1, 0), (0, 0, 0), (1, 1, 1)])
+def test_resolve_flag(flag, gpu, want):
+    assert A.resolve_flag(flag, bool(gpu)) == bool(want)
+
+
+@pytest.mark.parametrize("flag,gpu", [(1, 0), (2, 1), (-2, 0)])
+def test_resolve_flag_rejects(flag, gpu):
+    with pytest.raises(A.MlaM4Error) as e:
+        A.resolve_flag(flag, bool(gpu))
+    assert e.value.status == -6
+
+
+# ------------------------------------------------------------------ descriptors (host memory)
+def decode_tensors(n_kv=1024, H=32, nt=1, dk=576, dv=512, dtype=torch.float16):
+    kc = torch.zeros((n_kv, dk), dtype=dtype)
+    q = torch.zeros((nt, H, dk), dtype=torch.float32)
+    mask = torch.zeros((nt, n_kv), dtype=torch.float32)
+    out = torch.zeros((H, nt, dv), dtype=torch.float32)
+    return kc, q, mask, out
+
+
+def test_supports_kqkv_accepts_both_geometries_and_types():
+    assert A.supports_kqkv(*decode_tensors())
+    assert A.supports_kqkv(*decode_tensors(dk=320, dv=256))
+    assert A.supports_kqkv(*decode_tensors(dtype=torch.float32))
+    kc, q, _, out = decode_tensors(nt=4, H=8)
+    assert A.supports_kqkv(kc, q, None, out)                  # no mask
+
+
+def test_supports_kqkv_rejects_contract_violations():
+    kc, q, mask, out = decode_tensors()
+    assert not A.supports_kqkv(kc, q, mask, torch.zeros((32, 1, 511)))           # D_v not a multiple of 4
+    assert not A.supports_kqkv(kc, q, mask, torch.zeros((32, 2, 512)))           # nt mismatch
+    assert not A.supports_kqkv(kc, q[:, :, :320].contiguous(), mask, out)        # D_k mismatch
+    assert not A.supports_kqkv(kc, q, mask[:, :1000], out)                       # mask width != n_kv
+    assert not A.supports_kqkv(kc, q.half(), mask, out)                          # q must be F32
+    big = torch.zeros((1024, 580), dtype=torch.float16)
+    assert not A.supports_kqkv(big[:, 1:577], q, mask, out)                      # misaligned rows
+    assert not A.supports_kqkv(torch.zeros((1024, 1100), dtype=torch.float16), torch.zeros((1, 32, 1100)),
+                               mask, torch.zeros((32, 1, 512)))                   # D_k > 1024
+
+
+def test_supports_wkb():
+    w = torch.zeros((32, 512, 128))
+    q = torch.zeros((1, 32, 192))
+    qcur = torch.zeros((1, 32, 576))
+    assert A.supports_wkb(w, q[:, :, :128], qcur[:, :, :512])      # strided views, as the engine uses
+    assert not A.supports_wkb(w, q[:, :, :64], qcur[:, :, :512])   # d_n mismatch
+    assert not A.supports_wkb(torch.zeros((32, 512, 96)), torch.zeros((1, 32, 96)), qcur[:, :, :512])  # d_n 96
+
+
+def test_supports_phase():
+    G, S, dv = 1, 256, 512
+    part = torch.zeros((G, 1, S, ops.part_floats(dv)))
+    out = torch.zeros((32, 1, dv))
+    assert A.supports_phase(ops.PHASE_MERGE, part, out)
+    assert A.supports_phase(ops.PHASE_MERGE, torch.zeros((G, 1, S, ops.part_floats(dv, False))), out)
+    assert not A.supports_phase(ops.PHASE_MERGE, torch.zeros((G, 1, S, 1000)), out)
+    assert not A.supports_phase(ops.PHASE_MERGE, torch.zeros((G, 1, 1025, ops.part_floats(dv))), out)
+    assert not A.supports_phase(ops.PHASE_KVWRITE, part, out)     # phases 0 and 1: not in this library
+    assert not A.supports_phase(ops.PHASE_WVB, part, out)
+    assert not A.supports_phase(7, part, out)
+
+
+def test_default_splits_and_workspace(lib):
+    assert A.default_splits(32768) == 256
+    assert A.default_splits(64) == 1
+    assert 1 <= A.default_splits(4096) <= 64                     # at most one split per 64-key tile
+    assert A.default_splits(262144) <= ops.MAX_SPLITS
+    assert lib.mla_m4_kqkv_default_splits(0, 32, 1) == -6
+    kc, q, _, out = decode_tensors(n_kv=32768)
+    S = A.default_splits(32768)
+    assert A.kqkv_workspace_bytes(kc, q, out) == S * ops.part_floats(512) * 4
+    kc, q, _, out = decode_tensors(n_kv=64)
+    assert A.kqkv_workspace_bytes(kc, q, out) == 0                 # one split: no partials
+
+
+def test_entry_points_reject_before_launching(lib):
+    kc, q, mask, out = decode_tensors()
+    vk, vq, vm, vo = (ops.view(t) for t in (kc, q, mask, out))
+    P = ctypes.byref
+    assert lib.mla_m4_kqkv(None, P(vq), P(vm), ctypes.c_float(0.1), P(vo), None, 0, None) == -1
+    assert lib.mla_m4_kqkv(P(vk), P(vq), P(vm), ctypes.c_float(float("nan")), P(vo), None, 0, None) == -6
+    # split-K shapes need a workspace
+    assert lib.mla_m4_kqkv(P(vk), P(vq), P(vm), ctypes.c_float(0.1), P(vo), None, 0, None) == -5
+    part = ops.view(torch.zeros((1, 1, 8, ops.part_floats(512))))
+    assert lib.mla_m4_kqkv_partial(P(vk), P(vq), P(vm), ctypes.c_float(0.1), 0, 512, P(part), None) == -6
+    assert lib.mla_m4_kqkv_partial(P(vk), P(vq), P(vm), ctypes.c_float(0.1), 9, 512, P(part), None) == -3
+    assert lib.mla_m4_kqkv_partial(P(vk), P(vq), P(vm), ctypes.c_float(0.1), 8, 512, None, None) == -1
+    w = ops.view(torch.zeros((32, 512, 128)))
+    assert lib.mla_m4_wkb(P(w), None, P(vo), None) == -1
+    assert lib.mla_m4_phase_merge(None, P(vo), None) == -1
+
+
+def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
+    """Without the built library every op raises instead of computing anything on the host."""
+    monkeypatch.setattr(ops, "_lib", None)
+    monkeypatch.setattr(ops, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        A.ggml_m4_wkb(torch.zeros((32, 512, 128)), torch.zeros((1, 32, 128)))
