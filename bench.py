@@ -32,6 +32,8 @@ sys.path.insert(0, str(ROOT))
 METRIC = "µs/decode-step + achieved HBM GB/s (% peak) for MLA attention at 32K keys"
 HBM_PEAK_GBPS = 8000.0
 N_ROT = 12
+CAL_BYTES = 256 << 20          # calibration copy size (each way) for the HBM traffic counters
+TRAFFIC_FILE = ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json"
 
 
 def parse():
@@ -44,6 +46,8 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time S in {64,128,192,256}")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm", action="store_true", help="also report WARM (one cache) timings")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="no timing: run the calibration copy and a few steps, for rocprofv3 --pmc")
     return ap.parse_args()
 
 
@@ -98,6 +102,20 @@ def main() -> int:
         wkb(i)
         attn(i)
         merge()
+
+    if args.pmc_pass:
+        # the calibration kernel: a plain device copy of CAL_BYTES each way (torch's copy kernel),
+        # then N_ROT eager steps; rocprofv3 reports FETCH_SIZE / WRITE_SIZE per dispatch of each
+        src = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for i in range(N_ROT):
+            step(i)
+        torch.cuda.synchronize()
+        print(f"pmc pass done: copy {CAL_BYTES} B x3, {N_ROT} steps of config {args.config}, S={S}", flush=True)
+        return 0
 
     def capture(fn, n):
         g = torch.cuda.CUDAGraph()
@@ -192,6 +210,14 @@ def main() -> int:
                "sample": f"config {args.config} full step (WKB + unfused kq/softmax/kqv), median of 5 after 1 warm-up",
                "value_1thread": round(one * 1e6, 1)}
 
+    # HBM bytes per launch of the partial kernel, from the committed rocprofv3 counter summary
+    # (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the calibration copy's factor)
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        tr = json.loads(TRAFFIC_FILE.read_text())
+        if tr.get("config") == args.config and tr.get("splits") == S:
+            traffic = int(tr["traffic_bytes"])
+
     rec = {
         "metric": METRIC, "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1000.0, 6), "higher_is_better": False,
@@ -201,7 +227,7 @@ def main() -> int:
                                f"split-K S={S} + PHASE merge, COLD ({N_ROT} rotating copies), hipGraph",
                    "n_kv": W, "n_head": H, "d_k": DK, "d_v": DV, "splits": S, "seeds": inp.seeds, "notes": inp.notes},
         "roofline": {"bound": "hbm", "achieved": round(gbps_attn, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps_attn / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(gbps_attn / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": "kqkv_decode_f16_kernel<576,512>", "alg_bytes_per_launch": int(bytes_attn),
                      "us_per_launch": round(us_attn, 3)},
         "cpu_baseline": cpu,
