@@ -45,27 +45,32 @@ struct KqkvShape {
     bool has_mask;
 };
 
+// plan = true: the supports_op mirrors, called on descriptors whose data may not be allocated yet
+// (graph planning); only type/ne/nb are checked, and a data pointer only when it is set.
+bool has_data(const mla_m4_tensor * t, bool plan) { return t && (plan || t->data); }
+bool al16(const void * p, bool plan) { return (plan && !p) || aligned16(p); }
+
 int check_kqkv(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_tensor * mask,
-               const mla_m4_tensor * dst, KqkvShape * s) {
-    if (!kc || !q || !dst || !kc->data || !q->data || !dst->data) return MLA_M4_ERR_NULL;
+               const mla_m4_tensor * dst, KqkvShape * s, bool plan = false) {
+    if (!has_data(kc, plan) || !has_data(q, plan) || !has_data(dst, plan)) return MLA_M4_ERR_NULL;
     if (kc->type != MLA_M4_TYPE_F16 && kc->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
     if (q->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
     const size_t es = elsize(kc->type);
     // kcache ne [D_k, n_kv, 1, 1]
     if (kc->ne[0] < 1 || kc->ne[1] < 1 || kc->ne[2] != 1 || kc->ne[3] != 1) return MLA_M4_ERR_SHAPE;
-    if (kc->nb[0] != es || kc->nb[1] < (size_t)kc->ne[0] * es || (kc->nb[1] & 15u) || !aligned16(kc->data))
+    if (kc->nb[0] != es || kc->nb[1] < (size_t)kc->ne[0] * es || (kc->nb[1] & 15u) || !al16(kc->data, plan))
         return MLA_M4_ERR_STRIDE;
     // q ne [D_k, H, nt, 1]
     if (q->ne[0] != kc->ne[0] || q->ne[1] < 1 || q->ne[2] < 1 || q->ne[3] != 1) return MLA_M4_ERR_SHAPE;
-    if (q->nb[0] != 4 || (q->nb[1] & 15u) || (q->nb[2] & 15u) || !aligned16(q->data)) return MLA_M4_ERR_STRIDE;
+    if (q->nb[0] != 4 || (q->nb[1] & 15u) || (q->nb[2] & 15u) || !al16(q->data, plan)) return MLA_M4_ERR_STRIDE;
     if (q->nb[1] < (size_t)q->ne[0] * 4) return MLA_M4_ERR_STRIDE;
     // dst ne [D_v, nt, H, 1] contiguous
     const int64_t dv = dst->ne[0];
     if (dv < 4 || (dv & 3) || dv > kc->ne[0]) return MLA_M4_ERR_SHAPE;
     if (dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
-    if (!is_contiguous(dst) || !aligned16(dst->data)) return MLA_M4_ERR_STRIDE;
-    // mask ne [n_kv, >= nt, 1, 1] (optional)
-    const bool has_mask = mask && mask->data;
+    if (!is_contiguous(dst) || !al16(dst->data, plan)) return MLA_M4_ERR_STRIDE;
+    // mask ne [n_kv, >= nt, 1, 1] (optional: a null descriptor, or null data outside planning)
+    const bool has_mask = mask && (mask->data || (plan && mask->ne[0] > 0));
     if (has_mask) {
         if (mask->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
         if (mask->ne[0] != kc->ne[1] || mask->ne[1] < q->ne[2] || mask->ne[2] != 1 || mask->ne[3] != 1)
@@ -146,8 +151,8 @@ int launch_attn(const KqkvShape & s, const mla::DecodeArgs & a, hipStream_t stre
 }
 
 // ---------------------------------------------------------------- merge contract
-int check_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst) {
-    if (!part || !dst || !part->data || !dst->data) return MLA_M4_ERR_NULL;
+int check_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, bool plan = false) {
+    if (!has_data(part, plan) || !has_data(dst, plan)) return MLA_M4_ERR_NULL;
     if (part->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
     const int64_t dv = dst->ne[0];
     if (dv < 8 || (dv & 7) || dst->ne[1] < 1 || dst->ne[2] < 1 || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
@@ -156,22 +161,22 @@ int check_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst) {
         part->ne[2] != dst->ne[1] || part->ne[3] != n_groups_of(dst->ne[2]))
         return MLA_M4_ERR_SHAPE;
     if (dst->ne[1] > 65535 || dst->ne[2] > 65535) return MLA_M4_ERR_UNSUPPORTED;
-    if (!is_contiguous(part) || !is_contiguous(dst) || !aligned16(part->data) || !aligned16(dst->data))
+    if (!is_contiguous(part) || !is_contiguous(dst) || !al16(part->data, plan) || !al16(dst->data, plan))
         return MLA_M4_ERR_STRIDE;
     return MLA_M4_OK;
 }
 
 // ---------------------------------------------------------------- WKB contract
-int check_wkb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst) {
-    if (!w || !x || !dst || !w->data || !x->data || !dst->data) return MLA_M4_ERR_NULL;
+int check_wkb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst, bool plan = false) {
+    if (!has_data(w, plan) || !has_data(x, plan) || !has_data(dst, plan)) return MLA_M4_ERR_NULL;
     if (w->type != MLA_M4_TYPE_F32 || x->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32)
         return MLA_M4_ERR_TYPE;
     const int64_t dn = w->ne[0], dv = w->ne[1], nh = w->ne[2];
     if (dn < 1 || dv < 1 || nh < 1 || w->ne[3] != 1) return MLA_M4_ERR_SHAPE;
     if (x->ne[0] != dn || x->ne[1] != nh || x->ne[2] < 1 || x->ne[3] != 1) return MLA_M4_ERR_SHAPE;
     if (dst->ne[0] != dv || dst->ne[1] != nh || dst->ne[2] != x->ne[2] || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
-    if (!is_contiguous(w) || !aligned16(w->data)) return MLA_M4_ERR_STRIDE;
-    if (x->nb[0] != 4 || (x->nb[1] & 15u) || (x->nb[2] & 15u) || !aligned16(x->data)) return MLA_M4_ERR_STRIDE;
+    if (!is_contiguous(w) || !al16(w->data, plan)) return MLA_M4_ERR_STRIDE;
+    if (x->nb[0] != 4 || (x->nb[1] & 15u) || (x->nb[2] & 15u) || !al16(x->data, plan)) return MLA_M4_ERR_STRIDE;
     if (dst->nb[0] != 4 || (dst->nb[1] & 3u) || (dst->nb[2] & 3u)) return MLA_M4_ERR_STRIDE;
     if (dst->nb[1] < (size_t)dv * 4) return MLA_M4_ERR_STRIDE;
     if (dn != 64 && dn != 128) return MLA_M4_ERR_UNSUPPORTED;
@@ -296,17 +301,17 @@ int mla_m4_phase_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, vo
 }
 
 int mla_m4_supports_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope, const mla_m4_tensor * dst) {
-    return check_wkb(w, q_nope, dst) == MLA_M4_OK;
+    return check_wkb(w, q_nope, dst, true) == MLA_M4_OK;
 }
 
 int mla_m4_supports_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask,
                          const mla_m4_tensor * dst) {
     KqkvShape s{};
-    return check_kqkv(kcache, q, mask, dst, &s) == MLA_M4_OK;
+    return check_kqkv(kcache, q, mask, dst, &s, true) == MLA_M4_OK;
 }
 
 int mla_m4_supports_phase(int32_t phase, const mla_m4_tensor * src0, const mla_m4_tensor * dst) {
-    if (phase == MLA_M4_PHASE_MERGE) return check_merge(src0, dst) == MLA_M4_OK;
+    if (phase == MLA_M4_PHASE_MERGE) return check_merge(src0, dst, true) == MLA_M4_OK;
     return 0;   // phases 0 (KV-write) and 1 (wv_b) are not implemented by this library yet
 }
 

@@ -152,7 +152,10 @@ int mla_m4_phase_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, vo
 /* -------------------------------------------------------------------------------------------
  * supports_op mirrors (ggml-cuda.cu:5848-5885): 1 if the entry point above accepts these
  * tensors, 0 otherwise.  They run the same host-side contract checks as the launch, without
- * launching, so the backend's supports_op and the launcher cannot disagree.
+ * launching, so the backend's supports_op and the launcher cannot disagree.  Data pointers may
+ * be null (supports_op runs during graph planning, before allocation): only type, ne, nb and
+ * the alignment of pointers that are set are checked.  A mask descriptor with ne[0] > 0 counts
+ * as present.
  * ------------------------------------------------------------------------------------------- */
 int mla_m4_supports_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
                         const mla_m4_tensor * dst);

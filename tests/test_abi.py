@@ -84,6 +84,23 @@ def test_supports_kqkv_rejects_contract_violations():
                                mask, torch.zeros((32, 1, 512)))                   # D_k > 1024
 
 
+def test_supports_accept_unallocated_tensors():
+    """supports_op runs during graph planning, before the tensors have data."""
+    views = [ops.view(t) for t in decode_tensors()]
+    for v in views:
+        v.data = None
+    P = ctypes.byref
+    lib = A.load_library()
+    assert lib.mla_m4_supports_kqkv(P(views[0]), P(views[1]), P(views[2]), P(views[3])) == 1
+    views[3].ne[0] = 500
+    assert lib.mla_m4_supports_kqkv(P(views[0]), P(views[1]), P(views[2]), P(views[3])) == 0
+    part, out = ops.view(torch.zeros((1, 1, 4, ops.part_floats(512)))), ops.view(torch.zeros((32, 1, 512)))
+    part.data = out.data = None
+    assert lib.mla_m4_supports_phase(ops.PHASE_MERGE, P(part), P(out)) == 1
+    # the launch itself still rejects null data
+    assert lib.mla_m4_phase_merge(P(part), P(out), None) == -1
+
+
 def test_supports_wkb():
     w = torch.zeros((32, 512, 128))
     q = torch.zeros((1, 32, 192))
