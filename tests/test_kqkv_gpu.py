@@ -88,3 +88,21 @@ def test_partials_match_oracle(dev):
     assert np.allclose(m, ref[..., 0], atol=2e-3)
     assert np.allclose(l, ref[..., 1], rtol=2e-3)
     check("partials o/l", o, ref[..., 4:] / ref[..., 1:2], True)
+
+
+def test_prefill_cfg5_matches_oracle(dev):
+    """Config 5: 512 query tokens x 8192 keys, causal.  The GPU computes every token; the oracle
+    checks 48 of them (the first, middle and last 16: the shortest, a mid and the longest causal
+    windows), which keeps the CPU side to a few seconds."""
+    inp = I.make_config(5)
+    say(f"cfg5 nt={inp.nt} n_kv={inp.n_kv} {inp.notes}")
+    g = upload(inp, dev)
+    qcur, out = run_step(g, inp.kq_scale)
+    sel = np.r_[0:16, 248:264, inp.nt - 16:inp.nt]
+    check("cfg5 WKB/Qcur", qcur[sel, :, :I.D_V], orc.wkb(inp.w_kb, inp.q_nope[sel]), False)
+    qs = np.ascontiguousarray(qcur[sel])
+    ref = orc.kqkv(inp.kcache, qs, inp.mask[sel], inp.kq_scale)
+    check("cfg5 KQKV vs oracle", out[:, sel], ref, True)
+    hs = slice(0, 4)
+    ref64 = orc.attn_f64(inp.kcache, np.ascontiguousarray(qs[:, hs]), inp.mask[sel], inp.kq_scale)
+    check("cfg5 KQKV vs f64 (heads 0-3)", out[hs][:, sel], ref64, True, rel=TOL64[True])
