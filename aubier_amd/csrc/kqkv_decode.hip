@@ -24,6 +24,8 @@
 // Grid = (n_split, ceil(H/32), nt), 256 threads.  Output: one partial block per (32-head group,
 // token, split) -- m (the split's exact max) and l per head in f32 and the split's normalised
 // output o/l in f16, [32 heads][D_v] (mla_kernels.h) -- or, with a single split, o/l in f32 to dst.
+#include <type_traits>
+
 #include "mla_common.h"
 #include "mla_kernels.h"
 
@@ -155,17 +157,33 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     __syncthreads();
     half8 qreg[2][C::QSTEPS];   // [head tile n][step s]: head 16 n + j16, d = 32 s + 8 g .. +7
     {
+        // reads in batches of QB fragments ahead of their conversion (a read-convert chain per
+        // fragment would serialise on the LDS latency)
+        constexpr int QB = C::QSTEPS % 6 == 0 ? 6 : (C::QSTEPS % 5 == 0 ? 5 : 2);
+        static_assert(C::QSTEPS % QB == 0, "whole batches");
         const float * qs = reinterpret_cast<const float *>(ring + NWAVE * C::STAGE);
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
+        for (int n = 0; n < 2; ++n) {
+            const float * row = qs + 4 * (16 * n + j16) * C::QC;
 #pragma unroll
-            for (int s = 0; s < C::QSTEPS; ++s) {
-                const float * row = qs + 4 * (16 * n + j16) * C::QC;
-                const f32x4 x0 = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * s + 2 * g) ^ j16));
-                const f32x4 x1 = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * s + 2 * g + 1) ^ j16));
-                qreg[n][s] = half8{to_half(x0[0]), to_half(x0[1]), to_half(x0[2]), to_half(x0[3]),
-                                   to_half(x1[0]), to_half(x1[1]), to_half(x1[2]), to_half(x1[3])};
+            for (int s0 = 0; s0 < C::QSTEPS; s0 += QB) {
+                f32x4 x[QB][2];
+#pragma unroll
+                for (int b = 0; b < QB; ++b) {
+                    x[b][0] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g) ^ j16));
+                    x[b][1] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g + 1) ^ j16));
+                }
+#pragma unroll
+                for (int b = 0; b < QB; ++b) {
+                    half8 h = {to_half(x[b][0][0]), to_half(x[b][0][1]), to_half(x[b][0][2]), to_half(x[b][0][3]),
+                               to_half(x[b][1][0]), to_half(x[b][1][1]), to_half(x[b][1][2]), to_half(x[b][1][3])};
+                    // materialise the f16 fragment here: left alone, the compiler keeps the f32
+                    // values (twice the registers) and re-converts them at every use in the loop
+                    asm volatile("" : "+v"(h));
+                    qreg[n][s0 + b] = h;
+                }
             }
+        }
     }
     __syncthreads();                         // the q staging in stage 1 is free again
 
@@ -199,10 +217,14 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         const int kbase = (t0 + k) * TK + WK * w;
 
         // S^T = K . Q^T : the wave's 16 keys (C rows) x 32 heads (C cols, two 16-wide tiles)
+        // two accumulator chains per head tile (even / odd K-steps), so consecutive MFMAs never
+        // wait on each other's result
         f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-        {
-            // operand reads run QPF steps ahead of the MFMAs that consume them; the scheduling
-            // barriers keep the compiler from sinking them back next to their use
+        f32x4 acc2 = {0.f, 0.f, 0.f, 0.f}, acc3 = {0.f, 0.f, 0.f, 0.f};
+        // operand reads run QPF steps ahead of the MFMAs that consume them; the scheduling
+        // barriers keep the compiler from sinking them back next to their use.  Two copies of the
+        // loop (with and without the next tile's DMA) keep branches out of the steps.
+        auto qk = [&](auto with_dma) {
             constexpr int QPF = 4;
             const char * abase = sb + 16 * slot_of(j16, g);     // row j16, chunk 4 s + g of block s
             half8 abuf[QPF];
@@ -212,15 +234,25 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
             for (int s = 0; s < C::QSTEPS; ++s) {
                 const half8 av = abuf[s % QPF];
                 if (s + QPF < C::QSTEPS) abuf[s % QPF] = *reinterpret_cast<const half8 *>(abase + 1024 * (s + QPF));
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc1, 0, 0, 0);
-                if (pf && s <= C::DMA_N) put(dn, s);
+                if (s & 1) {
+                    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc2, 0, 0, 0);
+                    acc3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc3, 0, 0, 0);
+                } else {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc1, 0, 0, 0);
+                }
+                if constexpr (decltype(with_dma)::value)
+                    if (s <= C::DMA_N) put(dn, s);
                 __builtin_amdgcn_sched_barrier(0);
             }
+            if constexpr (decltype(with_dma)::value) {
 #pragma unroll
-            for (int i = C::QSTEPS; i <= C::DMA_N; ++i)
-                if (pf) put(dn, i);
-        }
+                for (int i = C::QSTEPS; i <= C::DMA_N; ++i) put(dn, i);
+            }
+        };
+        if (pf) qk(std::true_type{}); else qk(std::false_type{});
+        acc0 += acc2;
+        acc1 += acc3;
         // scores (log2 units) of keys 4 g + r for heads j16 (n = 0) and 16 + j16 (n = 1)
         const f32x4 mk = *reinterpret_cast<const f32x4 *>(sb + C::ROWS_BYTES + 16 * g);
         float sc[2][4];
@@ -281,19 +313,19 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
                 m_ref[n] = mv ? tm[n] : m_ref[n];
                 l_part[n] *= al[n];
             }
-            // accumulator rows are heads 8 (r / 4) + 4 (lane >> 5) + (r & 3): fetch their factors
-            // from the lanes holding them (head h's factor sits in lane h & 15 of set n = h >> 4)
-            f32x16 al16;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int h = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const float a0 = __shfl(al[0], h & 15, 64), a1 = __shfl(al[1], h & 15, 64);
-                al16[r] = (h >> 4) ? a1 : a0;
-            }
-            // In place on the accumulator registers, one asm block per element, so that they stay
-            // in AGPRs across this branch (a plain multiply makes the register allocator move the
-            // tile set through VGPRs).  The s_nops cover the MFMA -> VALU read distance.
             if (k > 0) {                          // (on the first tile the accumulators are still 0)
+                // accumulator rows are heads 8 (r / 4) + 4 (lane >> 5) + (r & 3): fetch their
+                // factors from the lanes holding them (head h's in lane h & 15 of set n = h >> 4)
+                f32x16 al16;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int h = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    const float a0 = __shfl(al[0], h & 15, 64), a1 = __shfl(al[1], h & 15, 64);
+                    al16[r] = (h >> 4) ? a1 : a0;
+                }
+                // In place on the accumulator registers, one asm block per element, so that they
+                // stay in AGPRs across this branch (a plain multiply makes the register allocator
+                // move the tile set through VGPRs).  The s_nops cover the MFMA -> VALU read distance.
                 asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
                 for (int i = 0; i < C::NTQ; ++i)
@@ -414,7 +446,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         const half4 lo = lds_read_tr16(reinterpret_cast<const half_t *>(reg + dv_lo * 64 + 8 * (u ^ ounit(dv_lo))));
         const half4 hi = lds_read_tr16(reinterpret_cast<const half_t *>(reg + dv_hi * 64 + 8 * (u ^ ounit(dv_hi))));
         const half8 hv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<half8 *>(blk + 256 + ((size_t)(16 * hb + je) * DV + C::DVQ * w + 8 * dv8) * 2) = hv;
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hv),
+                                    reinterpret_cast<u32x4 *>(blk + 256 + ((size_t)(16 * hb + je) * DV + C::DVQ * w + 8 * dv8) * 2));
     }
 }
 
