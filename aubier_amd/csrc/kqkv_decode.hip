@@ -84,7 +84,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     using C = DecodeCfg<DK, DV>;
     __shared__ __attribute__((aligned(16))) char ring[C::RING];          // [stage][wave] K rows + mask
     __shared__ __attribute__((aligned(16))) half_t px[2][HG * C::PROW];  // P exchange, by tile parity
-    __shared__ __attribute__((aligned(16))) float red[2][NWAVE][HG];     // slice maxima, by tile parity
+    __shared__ __attribute__((aligned(16))) float red[2][HG][NWAVE];     // slice maxima [head][wave], by tile parity
     __shared__ float fin_t[NWAVE][HG];
     __shared__ float fin_l[NWAVE][HG];
     __shared__ float fin_r[HG];
@@ -290,8 +290,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         };
         put_p();
         if (lane < 16) {
-            red[par][w][lane] = mx[0];
-            red[par][w][16 + lane] = mx[1];
+            red[par][lane][w] = mx[0];
+            red[par][16 + lane][w] = mx[1];
         }
         __syncthreads();
         // the tile's max per head; every wave reads the same values and holds the same reference,
@@ -300,8 +300,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         float tm[2];
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
-            tm[n] = fmaxf(fmaxf(red[par][0][16 * n + j16], red[par][1][16 * n + j16]),
-                          fmaxf(red[par][2][16 * n + j16], red[par][3][16 * n + j16]));
+            const f32x4 r4 = *reinterpret_cast<const f32x4 *>(&red[par][16 * n + j16][0]);
+            tm[n] = fmaxf(fmaxf(r4[0], r4[1]), fmaxf(r4[2], r4[3]));
             move |= (m_ref[n] == -INFINITY) ? (tm[n] != -INFINITY) : (tm[n] > m_ref[n] + LAZY);
         }
         if (__builtin_amdgcn_ballot_w64(move) != 0) {     // rare: move the reference, rescale, redo P
@@ -343,17 +343,29 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
 #pragma unroll
         for (int n = 0; n < 2; ++n) l_part[n] += (p[n][0] + p[n][1]) + (p[n][2] + p[n][3]);
 
-        // O[:, own columns] += P . V over the tile's 64 keys (4 slices x 16)
+        // O[:, own columns] += P . V over the tile's 64 keys (4 slices x 16); the operands of
+        // slice ks + 1 are read while the MFMAs of slice ks run
+        {
+            half8 pa[2], vb[2][C::NTQ];
+            auto load = [&](int ks, int b) {
+                pa[b] = *reinterpret_cast<const half8 *>(&pxv[(lane & 31) * C::PROW + WK * ks + 8 * (lane >> 5)]);
+                const char * vs = ring + stage_off(par, ks);
 #pragma unroll
-        for (int ks = 0; ks < NWAVE; ++ks) {
-            const half8 pa = *reinterpret_cast<const half8 *>(&pxv[(lane & 31) * C::PROW + WK * ks + 8 * (lane >> 5)]);
-            const char * vs = ring + stage_off(par, ks);
+                for (int i = 0; i < C::NTQ; ++i) {
+                    const half4 lo = lds_read_tr16(reinterpret_cast<const half_t *>(vs + pv_lo + 1024 * i));
+                    const half4 hi = lds_read_tr16(reinterpret_cast<const half_t *>(vs + pv_hi + 1024 * i));
+                    vb[b][i] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            };
+            load(0, 0);
 #pragma unroll
-            for (int i = 0; i < C::NTQ; ++i) {
-                const half4 lo = lds_read_tr16(reinterpret_cast<const half_t *>(vs + pv_lo + 1024 * i));
-                const half4 hi = lds_read_tr16(reinterpret_cast<const half_t *>(vs + pv_hi + 1024 * i));
-                const half8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, vb, o[i], 0, 0, 0);
+            for (int ks = 0; ks < NWAVE; ++ks) {
+                if (ks + 1 < NWAVE) load(ks + 1, (ks + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < C::NTQ; ++i)
+                    o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[ks & 1], vb[ks & 1][i], o[i], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
