@@ -1,0 +1,125 @@
+// mla_merge.h -- the split-K merge of one unit (64 output columns of one head of one token),
+// shared by the PHASE merge kernel and the decode kernel's fused merge (mla_kernels.h describes
+// the partial blocks).  The combine of patches/ggml-m4/m4-kqkv.cu:314-338: m* = max m_s,
+// l* = sum l_s e^(m_s - m*), o* = sum l_s e^(m_s - m*) (o_s / l_s), out = o* / l* (0 if every split
+// is empty).
+#pragma once
+
+#include "mla_common.h"
+#include "mla_kernels.h"
+
+namespace mla {
+
+// Scratch for one unit's cross-wavefront fold (LDS, 16-byte aligned).
+struct MergeScratch {
+    float sm[4][8];
+    float sL[4][8];
+    f32x4 sO[4][8][2];
+};
+
+// One workgroup (256 threads) per unit: 8 column-lanes (8 f16 columns = 16 bytes
+// each) x 32 split-lanes.  Split-lane sl takes splits sl, sl + 32, ...: the loads of a 256-split
+// chunk (16 bytes of o/l plus m, l) all issue before the first use, then the chunk is folded with
+// the max taken first.  Split-lanes are combined with wavefront shuffles, then across the four
+// wavefronts through LDS.  Accumulators: (m, L = sum l_s e^(m_s - m), O = sum l_s e^(m_s - m) o_s).
+template <typename OT>
+__device__ __forceinline__ void merge_unit(const char * __restrict__ part, int dv, int n_split, int nt, int cblk, int h,
+                                           int t, float * __restrict__ dst, MergeScratch & sc) {
+    float (&sm)[4][8] = sc.sm;
+    float (&sL)[4][8] = sc.sL;
+    f32x4 (&sO)[4][8][2] = sc.sO;
+
+    constexpr int J = 8;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c8 = tid & 7, sl_i = tid >> 3;               // column lane, split lane (0..31)
+    const int c = cblk * 64 + 8 * c8;
+    const int hh = h % PART_HEADS;
+    const size_t bb = part_block_bytes(dv, (int)sizeof(OT));
+    const char * base = part + ((size_t)(h / PART_HEADS) * nt + t) * n_split * bb;
+    const int cc = min(c, dv - 8);
+
+    float m = -INFINITY, L = 0.0f;
+    float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n_split; s0 += 32 * J) {
+        float ms[J], ls[J];
+        float os[J][8];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int s = s0 + 32 * j + sl_i;
+            const char * blk = base + (size_t)min(s, n_split - 1) * bb;
+            const float mv = reinterpret_cast<const float *>(blk)[hh];
+            ms[j] = (s < n_split) ? mv : -INFINITY;
+            ls[j] = reinterpret_cast<const float *>(blk)[PART_HEADS + hh];
+            const OT * src = reinterpret_cast<const OT *>(blk + 256) + (size_t)hh * dv + cc;
+            if constexpr (sizeof(OT) == 2) {
+                const half8 v = *reinterpret_cast<const half8 *>(src);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) os[j][k] = (float)v[k];
+            } else {
+                const f32x4 v0 = *reinterpret_cast<const f32x4 *>(src);
+                const f32x4 v1 = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) { os[j][k] = v0[k]; os[j][4 + k] = v1[k]; }
+            }
+        }
+        float mx = m;
+#pragma unroll
+        for (int j = 0; j < J; ++j) mx = fmaxf(mx, ms[j]);
+        const float f0 = (m == -INFINITY) ? 0.0f : exp2_fast((m - mx) * LOG2E);
+        L *= f0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) O[k] *= f0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const float f = (ms[j] == -INFINITY) ? 0.0f : ls[j] * exp2_fast((ms[j] - mx) * LOG2E);
+            L += f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) O[k] += f * os[j][k];
+        }
+        m = mx;
+    }
+    // fold the 8 split-lanes of this wavefront (lane bits 3..5)
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        const float m2 = shfl_xor(m, off);
+        const float L2 = shfl_xor(L, off);
+        const float M = fmaxf(m, m2);
+        const float f1 = (m == -INFINITY) ? 0.0f : exp2_fast((m - M) * LOG2E);
+        const float f2 = (m2 == -INFINITY) ? 0.0f : exp2_fast((m2 - M) * LOG2E);
+        L = L * f1 + L2 * f2;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) O[k] = O[k] * f1 + shfl_xor(O[k], off) * f2;
+        m = M;
+    }
+    if (lane < 8) {
+        sm[w][c8] = m;
+        sL[w][c8] = L;
+        sO[w][c8][0] = f32x4{O[0], O[1], O[2], O[3]};
+        sO[w][c8][1] = f32x4{O[4], O[5], O[6], O[7]};
+    }
+    __syncthreads();
+    if (tid < 8 && c < dv) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) M = fmaxf(M, sm[i][c8]);
+        f32x4 r0 = {0.f, 0.f, 0.f, 0.f}, r1 = {0.f, 0.f, 0.f, 0.f};
+        if (M > -INFINITY) {
+            float LL = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float f = (sm[i][c8] == -INFINITY) ? 0.0f : exp2_fast((sm[i][c8] - M) * LOG2E);
+                LL += sL[i][c8] * f;
+                r0 += sO[i][c8][0] * f;
+                r1 += sO[i][c8][1] * f;
+            }
+            const float inv = 1.0f / LL;
+            r0 *= inv;
+            r1 *= inv;
+        }
+        float * d = dst + ((size_t)h * nt + t) * dv + c;
+        *reinterpret_cast<f32x4 *>(d) = r0;
+        *reinterpret_cast<f32x4 *>(d + 4) = r1;
+    }
+}
+
+}  // namespace mla
