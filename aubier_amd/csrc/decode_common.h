@@ -1,0 +1,260 @@
+// decode_common.h -- the parts shared by the two split-K decode kernels (kqkv_decode.hip for
+// splits of a few tiles, kqkv_decode_long.hip for long splits): the KV slice geometry and its LDS
+// slot layout, the slice DMA, the q staging prologue and the Q.K^T step.
+//
+// A split is a run of whole 64-key tiles; wave w of the workgroup owns keys 16 w .. 16 w + 15 of
+// every tile (its "slice") and streams them into its own slot of a two-stage LDS ring by bounds-
+// checked LDS DMA (buffer_load_dwordx4 ... lds: no staging registers; rows at or past n_kv read as
+// zeros).  The workgroup covers a 32-head group; q enters Q.K^T as f16 fragments held in VGPRs.
+#pragma once
+
+#include <type_traits>
+
+#include "mla_common.h"
+#include "mla_kernels.h"
+
+namespace mla {
+namespace decode {
+
+constexpr int TK = 64;          // keys per split tile (splits are whole tiles)
+constexpr int NWAVE = 4;
+constexpr int NTHR = 64 * NWAVE;
+constexpr int WK = TK / NWAVE;  // keys per wave slice
+constexpr int HG = 32;          // heads per workgroup
+constexpr float LAZY = 8.0f;    // log2 slack before a reference max moves
+constexpr half2 ONE2 = {1.0f16, 1.0f16};
+
+template <int DK>
+struct SliceGeom {
+    static_assert(DK % 64 == 0, "geometry");
+    static constexpr int CH = DK * 2 / 16;              // 16-byte chunks per cache row
+    static_assert(CH % 4 == 0, "1 KB slot blocks of 4 chunks x 16 rows");
+    static constexpr int DMA_N = WK * CH / 64;          // 16-byte DMA instructions per slice
+    static constexpr int ROWS_BYTES = WK * DK * 2;
+    static constexpr int STAGE = ROWS_BYTES + 256;      // 16 K rows + the mask slot
+    static constexpr int RING = 2 * NWAVE * STAGE;
+    static constexpr int QSTEPS = DK / 32;              // K-steps of the 16x16x32 MFMA
+    static constexpr int QC = DK / 4;                   // 16-byte f32 chunks per q row
+    static constexpr int QD = HG * QC / 64 / NWAVE;     // q DMA instructions per wave
+    static_assert(QC % 16 == 0 && (HG * QC) % (64 * NWAVE) == 0, "q staging swizzle, whole q DMA instructions");
+    static_assert(HG * DK * 4 <= NWAVE * STAGE, "the f32 q staging fits stage 1 of the ring");
+    static_assert(QSTEPS == DMA_N, "one DMA block per Q.K^T step");
+};
+
+// Slot layout (one wave slice, 16 cache rows): 1 KB blocks i = 0 .. CH/4 - 1, block i holding chunks
+// 4 i .. 4 i + 3 (16 bytes each) of the 16 rows, chunk 4 i + q of row r at slot 16 q + (r ^ 4 q).
+// DMA instruction i fills block i, lane l fetching row (l & 15) ^ 4 (l >> 4), chunk 4 i + (l >> 4),
+// so its global offset is lane-only plus 64 i.  The XOR keeps the Q.K^T reads (16 rows, one chunk)
+// and the transpose reads (4 rows x 4 chunks per 32 lanes) on distinct banks, at 128 or 256 bytes
+// per LDS clock alike.
+__device__ __forceinline__ int slot_of(int r, int q) { return 16 * q + (r ^ (4 * q)); }
+
+// Where the V^T / V operand of P.V comes from: two transpose reads per 32-column tile, in 16-lane
+// group g lane j supplying row 8 (g >> 1) + (j >> 2) (then + 4) of a slice, 4 columns at
+// 32 i + 16 (g & 1) + 4 (j & 3).  Lane l then holds column 32 i + (l & 31), keys 8 (l >> 5) .. +7.
+struct PvAddr {
+    int lo, hi;
+    __device__ __forceinline__ explicit PvAddr(int lane) {
+        const int g = lane >> 4, j16 = lane & 15;
+        const int r0 = 8 * (g >> 1) + (j16 >> 2);
+        const int cq = 2 * (g & 1) + ((j16 & 3) >> 1);
+        lo = 16 * slot_of(r0, cq) + 8 * (j16 & 1);
+        hi = 16 * slot_of(r0 + 4, cq) + 8 * (j16 & 1);
+    }
+    // the operand of 32-column tile i of the slice at sb
+    __device__ __forceinline__ half8 load(const char * sb, int i) const {
+        const half4 l4 = lds_read_tr16(reinterpret_cast<const half_t *>(sb + lo + 1024 * i));
+        const half4 h4 = lds_read_tr16(reinterpret_cast<const half_t *>(sb + hi + 1024 * i));
+        return half8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+    }
+};
+
+struct SliceDma { i32x4 krs, mrs; uint32_t sb; };
+
+// The wave's view of its split: tile range, DMA of its slice of tile k into stage s.
+template <int DK>
+struct SliceStream {
+    using G = SliceGeom<DK>;
+    const char * kc;
+    int64_t kc_nb1;
+    const float * mrow;     // this token's mask row (or any valid pointer when there is none)
+    bool has_mask;
+    int n_kv, n_tiles, t0, n_my, w;
+    uint32_t ring_lds, kvoff, mvoff;
+
+    __device__ __forceinline__ SliceStream(const DecodeArgs & a, int sp, int t, int w_, uint32_t ring_lds_, int lane) {
+        kc = a.kc;
+        kc_nb1 = a.kc_nb1;
+        has_mask = a.mask != nullptr;
+        mrow = has_mask ? reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) + (size_t)t * a.mask_nb1) : a.q;
+        n_kv = a.n_kv;
+        n_tiles = a.n_tiles;
+        // balanced partition of whole 64-key tiles over the splits
+        const int base_t = a.n_tiles / a.n_split;
+        const int rem = a.n_tiles % a.n_split;
+        t0 = sp * base_t + min(sp, rem);
+        n_my = base_t + (sp < rem ? 1 : 0);
+        w = w_;
+        ring_lds = ring_lds_;
+        kvoff = (uint32_t)(((lane & 15) ^ (4 * (lane >> 4))) * kc_nb1) + 16u * (uint32_t)(lane >> 4);
+        mvoff = 4u * (uint32_t)(lane & 15);
+    }
+    __device__ __forceinline__ int stage_off(int s, int v) const { return (s * NWAVE + v) * G::STAGE; }
+    // The resources are rebased on the slice, num_records = bytes up to the end of row n_kv - 1, so
+    // rows (and mask entries) at or past n_kv come back as zeros.  k is clamped into the split (a
+    // split with no tile re-reads a valid one and never uses it).
+    __device__ __forceinline__ SliceDma plan(int s, int k) const {
+        const int tile = min(t0 + min(k, n_my - 1), n_tiles - 1);
+        const int key0 = tile * TK + WK * w;
+        const int left = n_kv - key0;                    // rows of this slice that exist (may be <= 0)
+        SliceDma d;
+        d.krs = make_rsrc(kc + (int64_t)key0 * kc_nb1, left > 0 ? (uint32_t)((int64_t)(left - 1) * kc_nb1 + DK * 2) : 0u);
+        d.mrs = make_rsrc(mrow + key0, (has_mask && left > 0) ? (uint32_t)left * 4u : 0u);
+        d.sb = ring_lds + (uint32_t)stage_off(s, w);
+        return d;
+    }
+    // instruction i < DMA_N: block i of the rows; i == DMA_N: the mask slot (float l = key key0 + (l & 15))
+    __device__ __forceinline__ void put(const SliceDma & d, int i) const {
+        if (i < G::DMA_N) dma16_nt(d.krs, kvoff, (uint32_t)(64 * i), d.sb + (uint32_t)(1024 * i));
+        else dma4(d.mrs, mvoff, 0u, d.sb + (uint32_t)G::ROWS_BYTES);
+    }
+};
+
+// q block (32 heads x DK f32) -> stage 1 of the ring by DMA, tile 0's slice -> stage 0 behind it,
+// then f16 B fragments in registers: qreg[n][s] = head 16 n + j16, d = 32 s + 8 g .. +7.  Staging
+// slot of f32 chunk c (4 floats) of head h: h * QC + (c ^ (h & 15)), so the fragment reads (16
+// heads, one chunk) hit distinct banks; heads past n_head read as zeros.  Ends with a barrier
+// after which stage 1 is free; the slice DMA of tile 0 (DMA_N + 1 instructions) may still be in flight.
+template <int DK>
+__device__ __forceinline__ void stage_q(const DecodeArgs & a, const SliceStream<DK> & ss, char * ring, int hg0, int t,
+                                        int lane, half8 (&qreg)[2][SliceGeom<DK>::QSTEPS]) {
+    using G = SliceGeom<DK>;
+    const int w = ss.w;
+    const int g = lane >> 4, j16 = lane & 15;
+    {
+        const int nh = min(HG, a.n_head - hg0);
+        const i32x4 qrs = make_rsrc(reinterpret_cast<const char *>(a.q) + (size_t)t * a.q_nb2 + (size_t)hg0 * a.q_nb1,
+                                    (uint32_t)((int64_t)(nh - 1) * a.q_nb1 + DK * 4));
+        const uint32_t qsb = ss.ring_lds + (uint32_t)(NWAVE * G::STAGE);
+#pragma unroll
+        for (int i = 0; i < G::QD; ++i) {
+            const int p = (w * G::QD + i) * 64 + lane;
+            const int h = p / G::QC;
+            const int c = (p - h * G::QC) ^ (h & 15);
+            dma16(qrs, (uint32_t)(h * a.q_nb1) + 16u * (uint32_t)c, 0u, qsb + (uint32_t)((w * G::QD + i) * 1024));
+        }
+        const SliceDma d0 = ss.plan(0, 0);
+#pragma unroll
+        for (int i = 0; i <= G::DMA_N; ++i) ss.put(d0, i);
+    }
+    wait_vm<G::DMA_N + 1>();                 // this wave's part of q has landed
+    __syncthreads();
+    {
+        // reads in batches of QB fragments ahead of their conversion (a read-convert chain per
+        // fragment would serialise on the LDS latency)
+        constexpr int QB = G::QSTEPS % 6 == 0 ? 6 : (G::QSTEPS % 5 == 0 ? 5 : 2);
+        static_assert(G::QSTEPS % QB == 0, "whole batches");
+        const float * qs = reinterpret_cast<const float *>(ring + NWAVE * G::STAGE);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const float * row = qs + 4 * (16 * n + j16) * G::QC;
+#pragma unroll
+            for (int s0 = 0; s0 < G::QSTEPS; s0 += QB) {
+                f32x4 x[QB][2];
+#pragma unroll
+                for (int b = 0; b < QB; ++b) {
+                    x[b][0] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g) ^ j16));
+                    x[b][1] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g + 1) ^ j16));
+                }
+#pragma unroll
+                for (int b = 0; b < QB; ++b) {
+                    half8 h = {to_half(x[b][0][0]), to_half(x[b][0][1]), to_half(x[b][0][2]), to_half(x[b][0][3]),
+                               to_half(x[b][1][0]), to_half(x[b][1][1]), to_half(x[b][1][2]), to_half(x[b][1][3])};
+                    // materialise the f16 fragment here: left alone, the compiler keeps the f32
+                    // values (twice the registers) and re-converts them at every use in the loop
+                    asm volatile("" : "+v"(h));
+                    qreg[n][s0 + b] = h;
+                }
+            }
+        }
+    }
+    __syncthreads();                         // the q staging in stage 1 is free again
+}
+
+// S^T = K . Q^T for the wave's 16 keys of the slice at sb (C rows = keys 4 g + r, C cols = heads
+// j16 (acc0) and 16 + j16 (acc1)).  DMA accounting (instructions complete in issue order): the
+// slice is DMA_N blocks then the mask; before the read of block b, the blocks after it, the mask
+// and the next slice's instructions issued so far (one per completed step) may still be in flight.
+// With DMA, the next slice's DMA (dn) is spread over the steps.  Operand reads run QPF steps ahead
+// of their MFMAs; the scheduling barriers keep the compiler from sinking them back next to their
+// use.  Two accumulator chains per head tile (even / odd steps) keep consecutive MFMAs
+// independent.  Returns with the slice's mask slot landed.
+template <int DK, bool DMA>
+__device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const SliceDma & dn, const char * sb, int lane,
+                                         const half8 (&qreg)[2][SliceGeom<DK>::QSTEPS], f32x4 & s0, f32x4 & s1) {
+    using G = SliceGeom<DK>;
+    constexpr int QPF = 4;
+    const int g = lane >> 4, j16 = lane & 15;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc2 = {0.f, 0.f, 0.f, 0.f}, acc3 = {0.f, 0.f, 0.f, 0.f};
+    const char * abase = sb + 16 * slot_of(j16, g);     // row j16, chunk 4 s + g of block s
+    half8 abuf[QPF];
+    wait_vm<G::DMA_N + 1 - QPF>();
+#pragma unroll
+    for (int s = 0; s < QPF; ++s) abuf[s] = *reinterpret_cast<const half8 *>(abase + 1024 * s);
+#pragma unroll
+    for (int s = 0; s < G::QSTEPS; ++s) {
+        const half8 av = abuf[s % QPF];
+        if (s + QPF < G::QSTEPS) {
+            if constexpr (DMA) wait_vm<G::DMA_N - QPF>();
+            else wait_vm_le(G::DMA_N - QPF - s);
+            abuf[s % QPF] = *reinterpret_cast<const half8 *>(abase + 1024 * (s + QPF));
+        }
+        if (s & 1) {
+            acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc2, 0, 0, 0);
+            acc3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc3, 0, 0, 0);
+        } else {
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc1, 0, 0, 0);
+        }
+        if constexpr (DMA) ss.put(dn, s);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (DMA) {
+        ss.put(dn, G::DMA_N);
+        wait_vm<G::DMA_N + 1>();             // the mask slot (the next slice's DMA_N + 1 may be in flight)
+    } else {
+        wait_vm<0>();
+    }
+    s0 = acc0 + acc2;
+    s1 = acc1 + acc3;
+}
+
+// Scores in log2 units of keys kbase + 4 g + r for heads j16 (sc[0]) and 16 + j16 (sc[1]); masked,
+// padded and out-of-range keys are -inf.  mx = the slice's max per head over its 16 keys.
+template <int DK>
+__device__ __forceinline__ void slice_scores(const DecodeArgs & a, const char * sb, int kbase, int lane, const f32x4 & s0,
+                                             const f32x4 & s1, float (&sc)[2][4], float (&mx)[2]) {
+    using G = SliceGeom<DK>;
+    const int g = lane >> 4;
+    const f32x4 mk = *reinterpret_cast<const f32x4 *>(sb + G::ROWS_BYTES + 16 * g);
+    mx[0] = -INFINITY;
+    mx[1] = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const bool live = kbase + 4 * g + r < a.n_kv;
+        const float mb = mk[r] * LOG2E;              // zeros when there is no mask
+        sc[0][r] = live ? s0[r] * a.scale_log2 + mb : -INFINITY;
+        sc[1][r] = live ? s1[r] * a.scale_log2 + mb : -INFINITY;
+        mx[0] = fmaxf(mx[0], sc[0][r]);
+        mx[1] = fmaxf(mx[1], sc[1][r]);
+    }
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        mx[n] = fmaxf(mx[n], shfl_xor(mx[n], 16));
+        mx[n] = fmaxf(mx[n], shfl_xor(mx[n], 32));
+    }
+}
+
+}  // namespace decode
+}  // namespace mla

@@ -9,6 +9,7 @@ namespace mla {
 typedef _Float16 half_t;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -80,6 +81,16 @@ __device__ __forceinline__ void dma4(i32x4 rsrc, uint32_t voff, uint32_t soff, u
 }
 template <int N>
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
+// s_waitcnt vmcnt(n) for an n that folds to a constant once the caller's loop is unrolled
+template <int N = 0>
+__device__ __forceinline__ void wait_vm_le(int n) {
+    if constexpr (N >= 63) {
+        wait_vm<63>();
+    } else {
+        if (n <= N) { wait_vm<N>(); return; }
+        wait_vm_le<N + 1>(n);
+    }
+}
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // 16-byte global load/store helpers

@@ -8,7 +8,9 @@
 namespace mla {
 
 // Split-K partial block of one (32-head group, token, split), blocks ordered [group][token][split]:
-//   float m[32]        running max of the split's scores (natural-log units; -inf if empty)
+//   float m[32]        a reference for the split's scores, natural-log units: the exact max
+//                      (VALU kernel) or a running reference at most 8 ln 2 below it (MFMA decode
+//                      kernel); -inf if the split is empty.  The merge only uses m + ln l.
 //   float l[32]        sum_j exp(s_j - m)
 //   T     o[32][D_v]   o / l: the split's normalised softmax output, 0 for an empty split.  T is
 //                      the cache's element type: f16 for an f16 cache (|o / l| <= max|V|, so it

@@ -84,9 +84,11 @@ def test_partials_match_oracle(dev):
     part = A.ggml_m4_kqkv_partial(g["kcache"], g["qcur"], g["mask"], inp.kq_scale, S)
     m, l, o = A.ops.decode_partials(part, I.N_HEAD)
     ref = orc.partials(inp.kcache, qcur, inp.mask, inp.kq_scale, orc.split_bounds(inp.n_kv, S))
-    # m within the f16 rounding of q in the scores; l to f32 accumulation; o/l to the f16 bar
-    assert np.allclose(m, ref[..., 0], atol=2e-3)
-    assert np.allclose(l, ref[..., 1], rtol=2e-3)
+    # A block's (m, l) is one representation of the split's log-sum-exp: the decode kernel's m is
+    # its shared reference maximum, at most 8 ln 2 below the split's max, with l relative to it.
+    # The merge depends on m + ln l only; that, the bound on m and o/l are what is checked.
+    assert np.all(m <= ref[..., 0] + 2e-3) and np.all(m >= ref[..., 0] - 8 * np.log(2) - 2e-3)
+    assert np.allclose(m + np.log(l), ref[..., 0] + np.log(ref[..., 1]), atol=2e-3)
     check("partials o/l", o, ref[..., 4:] / ref[..., 1:2], True)
 
 
