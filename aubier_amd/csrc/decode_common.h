@@ -188,10 +188,12 @@ __device__ __forceinline__ void stage_q(const DecodeArgs & a, const SliceStream<
 // With DMA, the next slice's DMA (dn) is spread over the steps.  Operand reads run QPF steps ahead
 // of their MFMAs; the scheduling barriers keep the compiler from sinking them back next to their
 // use.  Two accumulator chains per head tile (even / odd steps) keep consecutive MFMAs
-// independent.  Returns with the slice's mask slot landed.
-template <int DK, bool DMA>
+// independent.  Returns with the slice's mask slot landed.  WAIT = false: the slice is known to
+// be in LDS already (no DMA accounting, no next-slice DMA).
+template <int DK, bool DMA, bool WAIT = true>
 __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const SliceDma & dn, const char * sb, int lane,
                                          const half8 (&qreg)[2][SliceGeom<DK>::QSTEPS], f32x4 & s0, f32x4 & s1) {
+    static_assert(WAIT || !DMA, "a slice already in LDS comes with no DMA to spread");
     using G = SliceGeom<DK>;
     constexpr int QPF = 4;
     const int g = lane >> 4, j16 = lane & 15;
@@ -199,7 +201,7 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
     f32x4 acc2 = {0.f, 0.f, 0.f, 0.f}, acc3 = {0.f, 0.f, 0.f, 0.f};
     const char * abase = sb + 16 * slot_of(j16, g);     // row j16, chunk 4 s + g of block s
     half8 abuf[QPF];
-    wait_vm<G::DMA_N + 1 - QPF>();
+    if constexpr (WAIT) wait_vm<G::DMA_N + 1 - QPF>();
 #pragma unroll
     for (int s = 0; s < QPF; ++s) abuf[s] = *reinterpret_cast<const half8 *>(abase + 1024 * s);
 #pragma unroll
@@ -207,7 +209,7 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
         const half8 av = abuf[s % QPF];
         if (s + QPF < G::QSTEPS) {
             if constexpr (DMA) wait_vm<G::DMA_N - QPF>();
-            else wait_vm_le(G::DMA_N - QPF - s);
+            else if constexpr (WAIT) wait_vm_le(G::DMA_N - QPF - s);
             abuf[s % QPF] = *reinterpret_cast<const half8 *>(abase + 1024 * (s + QPF));
         }
         if (s & 1) {
@@ -223,7 +225,7 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
     if constexpr (DMA) {
         ss.put(dn, G::DMA_N);
         wait_vm<G::DMA_N + 1>();             // the mask slot (the next slice's DMA_N + 1 may be in flight)
-    } else {
+    } else if constexpr (WAIT) {
         wait_vm<0>();
     }
     s0 = acc0 + acc2;
@@ -231,13 +233,17 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
 }
 
 // Scores in log2 units of keys kbase + 4 g + r for heads j16 (sc[0]) and 16 + j16 (sc[1]); masked,
-// padded and out-of-range keys are -inf.  mx = the slice's max per head over its 16 keys.
+// padded and out-of-range keys are -inf.  mk = the mask values of those 4 keys (zeros without a
+// mask).  mx = the slice's max per head over its 16 keys.
+// the mask values of keys 4 g .. 4 g + 3 of the slice at sb (its mask slot)
 template <int DK>
-__device__ __forceinline__ void slice_scores(const DecodeArgs & a, const char * sb, int kbase, int lane, const f32x4 & s0,
+__device__ __forceinline__ f32x4 slice_mask(const char * sb, int lane) {
+    return *reinterpret_cast<const f32x4 *>(sb + SliceGeom<DK>::ROWS_BYTES + 16 * (lane >> 4));
+}
+
+__device__ __forceinline__ void slice_scores(const DecodeArgs & a, const f32x4 & mk, int kbase, int lane, const f32x4 & s0,
                                              const f32x4 & s1, float (&sc)[2][4], float (&mx)[2]) {
-    using G = SliceGeom<DK>;
     const int g = lane >> 4;
-    const f32x4 mk = *reinterpret_cast<const f32x4 *>(sb + G::ROWS_BYTES + 16 * g);
     mx[0] = -INFINITY;
     mx[1] = -INFINITY;
 #pragma unroll

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         if (k + 1 < n_my) qk_slice<DK, true>(ss, dn, sb, lane, qreg, s0, s1);
         else qk_slice<DK, false>(ss, dn, sb, lane, qreg, s0, s1);
         float sc[2][4], mx[2];
-        slice_scores<DK>(a, sb, kbase, lane, s0, s1, sc, mx);
+        slice_scores(a, slice_mask<DK>(sb, lane), kbase, lane, s0, s1, sc, mx);
         // P against the current reference (exact unless the reference moves below; the clamp only
         // keeps a provisional value finite), into the exchange as [32 heads][64 keys]
         half_t * pxv = px[par];

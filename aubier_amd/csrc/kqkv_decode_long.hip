@@ -84,7 +84,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
         if (k + 1 < n_my) qk_slice<DK, true>(ss, dn, sb, lane, qreg, s0, s1);
         else qk_slice<DK, false>(ss, dn, sb, lane, qreg, s0, s1);
         float sc[2][4], mx[2];
-        slice_scores<DK>(a, sb, kbase, lane, s0, s1, sc, mx);
+        slice_scores(a, slice_mask<DK>(sb, lane), kbase, lane, s0, s1, sc, mx);
         bool mv[2];
 #pragma unroll
         for (int n = 0; n < 2; ++n) mv[n] = (m_run[n] == -INFINITY) ? (mx[n] != -INFINITY) : (mx[n] > m_run[n] + LAZY);

@@ -146,9 +146,71 @@ hipError_t launch_kqkv_generic(int dk, int dv, int kc_is_f16, const DecodeArgs &
     return hipGetLastError();
 }
 
+// The PHASE merge for a few splits (chunked prefill: many tokens, S <= MERGE_FEW): one thread per
+// (token, head, 8 output columns) folding the S partials in order -- a wavefront covers 64 chunks
+// of one head's row, so every split's o / l is read as contiguous 1 KB (f16) and the header as a
+// broadcast.  The same combine as merge_unit: m* = max m_s, l* = sum l_s e^(m_s - m*),
+// out = sum l_s e^(m_s - m*) (o_s / l_s) / l*, 0 when every split is empty.
+constexpr int MERGE_FEW = 16;
+
+template <typename OT>
+__global__ __launch_bounds__(256) void merge_few_kernel(const char * __restrict__ part, int dv, int n_split, int nt,
+                                                        int n_head, float * __restrict__ dst) {
+    const int c8n = dv / 8;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)nt * n_head * c8n) return;
+    const int c8 = (int)(idx % c8n);
+    const int h = (int)((idx / c8n) % n_head);
+    const int t = (int)(idx / ((int64_t)c8n * n_head));
+    const int hh = h % PART_HEADS;
+    const size_t bb = part_block_bytes(dv, (int)sizeof(OT));
+    const char * base = part + ((size_t)(h / PART_HEADS) * nt + t) * n_split * bb;
+    float ms[MERGE_FEW], ls[MERGE_FEW];
+    float m = -INFINITY;
+    for (int s = 0; s < n_split; ++s) {
+        ms[s] = reinterpret_cast<const float *>(base + (size_t)s * bb)[hh];
+        ls[s] = reinterpret_cast<const float *>(base + (size_t)s * bb)[PART_HEADS + hh];
+        m = fmaxf(m, ms[s]);
+    }
+    float L = 0.0f;
+    float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < n_split; ++s) {
+        const float f = (ms[s] == -INFINITY) ? 0.0f : ls[s] * exp2_fast((ms[s] - m) * LOG2E);
+        L += f;
+        const OT * src = reinterpret_cast<const OT *>(base + (size_t)s * bb + 256) + (size_t)hh * dv + 8 * c8;
+        if constexpr (sizeof(OT) == 2) {
+            const half8 v = *reinterpret_cast<const half8 *>(src);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) O[k] += f * (float)v[k];
+        } else {
+            const f32x4 v0 = *reinterpret_cast<const f32x4 *>(src);
+            const f32x4 v1 = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { O[k] += f * v0[k]; O[4 + k] += f * v1[k]; }
+        }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    float * d = dst + ((size_t)h * nt + t) * dv + 8 * c8;
+    *reinterpret_cast<f32x4 *>(d) = f32x4{O[0] * inv, O[1] * inv, O[2] * inv, O[3] * inv};
+    *reinterpret_cast<f32x4 *>(d + 4) = f32x4{O[4] * inv, O[5] * inv, O[6] * inv, O[7] * inv};
+}
+
 hipError_t launch_merge(const char * part, int dv, int o_bytes, int n_split, int nt, int n_head, float * dst,
                         hipStream_t stream) {
     if (dv % 8 != 0) return hipErrorInvalidValue;
+    // few splits over many (token, head) rows: a thread per 8 columns; otherwise (decode: hundreds
+    // of splits, one token) a workgroup per 64 columns with the splits across its lanes
+    if (n_split <= MERGE_FEW && (int64_t)nt * n_head >= 256) {
+        const int64_t threads = (int64_t)nt * n_head * (dv / 8);
+        const dim3 grid((unsigned)((threads + 255) / 256));
+        if (o_bytes == 2)
+            hipLaunchKernelGGL(merge_few_kernel<half_t>, grid, dim3(256), 0, stream, part, dv, n_split, nt, n_head, dst);
+        else if (o_bytes == 4)
+            hipLaunchKernelGGL(merge_few_kernel<float>, grid, dim3(256), 0, stream, part, dv, n_split, nt, n_head, dst);
+        else
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     dim3 grid((dv + 63) / 64, n_head, nt);
     if (o_bytes == 2)
         hipLaunchKernelGGL(merge_kernel<half_t>, grid, dim3(256), 0, stream, part, dv, n_split, nt, dst);

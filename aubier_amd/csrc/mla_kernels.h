@@ -39,6 +39,11 @@ struct DecodeArgs {
 };
 
 hipError_t launch_kqkv_decode_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
+// several query tokens (nt >= PREFILL_MIN_TOKENS): 4 tokens per workgroup sharing each K / V tile;
+// grid (n_split, ceil(H/32), ceil(nt/4)); same outputs and geometries as the decode kernel
+constexpr int PREFILL_MIN_TOKENS = 4;
+constexpr int PREFILL_TOKENS_PER_WG = 4;
+hipError_t launch_kqkv_prefill_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
 bool decode_f16_supported(int dk, int dv);
 
 // Generic VALU path (f32 or f16 cache, any D_k <= 1024, D_v <= D_k): one workgroup per

@@ -98,12 +98,18 @@ bool use_mfma(const KqkvShape & s) {
     return s.kc_type == MLA_M4_TYPE_F16 && mla::decode_f16_supported((int)s.dk, (int)s.dv) && span <= 0xFFFFFFFFull;
 }
 
+// several tokens on the MFMA path: the prefill kernel (4 tokens per workgroup share each tile)
+bool use_prefill(const KqkvShape & s) { return use_mfma(s) && s.nt >= mla::PREFILL_MIN_TOKENS; }
+
 int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
 
 int default_splits(const KqkvShape & s) {
     const int64_t tiles = n_tiles_of(s.n_kv);
     int64_t groups;   // workgroups per split
-    if (use_mfma(s)) groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) * s.nt;
+    if (use_prefill(s))
+        groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) *
+                 ((s.nt + mla::PREFILL_TOKENS_PER_WG - 1) / mla::PREFILL_TOKENS_PER_WG);
+    else if (use_mfma(s)) groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) * s.nt;
     else groups = s.n_head * s.nt;
     int64_t sp = (TARGET_WG + groups - 1) / groups;
     if (sp > tiles) sp = tiles;
@@ -145,7 +151,8 @@ mla::DecodeArgs make_args(const mla_m4_tensor * kc, const mla_m4_tensor * q, con
 
 int launch_attn(const KqkvShape & s, const mla::DecodeArgs & a, hipStream_t stream) {
     hipError_t e;
-    if (use_mfma(s)) e = mla::launch_kqkv_decode_f16((int)s.dk, (int)s.dv, a, stream);
+    if (use_prefill(s)) e = mla::launch_kqkv_prefill_f16((int)s.dk, (int)s.dv, a, stream);
+    else if (use_mfma(s)) e = mla::launch_kqkv_decode_f16((int)s.dk, (int)s.dv, a, stream);
     else e = mla::launch_kqkv_generic((int)s.dk, (int)s.dv, s.kc_type == MLA_M4_TYPE_F16, a, stream);
     return e == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
 }

@@ -6,7 +6,8 @@
 // Decode is a pure HBM stream of W_kb (8 MiB at d_n = 128, D_v = 512, H = 32): each wavefront
 // owns 8 (d_n = 128) or 16 (d_n = 64) consecutive rows of one head, issues all its 16-byte row
 // loads before the first use, and reduces each row over its d_n/4 lanes with xor shuffles.  For
-// nt > 1 the rows stay in registers while the tokens stream past.
+// a few tokens the rows stay in registers while the tokens stream past; from 16 tokens on the op
+// is a batched GEMM and runs on f32 MFMA (wkb_gemm_kernel).
 #include "mla_common.h"
 #include "mla_kernels.h"
 
@@ -61,9 +62,92 @@ __global__ __launch_bounds__(256) void wkb_f32_kernel(WkbArgs a) {
     }
 }
 
+// Many tokens (chunked prefill): per head a GEMM dst_h[t][c] = sum_d q_h[t][d] W_h[c][d], on
+// v_mfma_f32_32x32x2_f32 (f32 products and sums, as the f32 mul_mat).  A workgroup computes 128
+// tokens x 128 columns of one head, each wave a 64 x 64 quarter (2 x 2 tiles of 32 x 32).  Both
+// operands have d contiguous, so a lane reads 4 consecutive d of its row (16 bytes) and spends them
+// on 4 MFMA k-steps: step j uses d = 8 p + 4 (lane >> 5) + j in A and B alike (the k order inside
+// an MFMA is free as long as both operands agree).  Operands come straight from global memory
+// (L2-resident: each q tile is read by D_v/128 workgroups, each W tile by nt/128) one 8-d block
+// ahead of their MFMAs.
+constexpr int WKB_GEMM_MIN_TOKENS = 16;
+
+__global__ __launch_bounds__(256) void wkb_gemm_kernel(WkbArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int h = blockIdx.z;
+    const int tw = blockIdx.y * 128 + 64 * (w >> 1);     // this wave's first token
+    const int cw = blockIdx.x * 128 + 64 * (w & 1);      // and first column
+    const int r32 = lane & 31, hh = lane >> 5;
+    const char * qb = reinterpret_cast<const char *>(a.q) + (size_t)h * a.q_nb1;
+    const float * wb = a.w + (size_t)h * a.d_v * a.d_n;
+    const float * arow[2];
+    const float * brow[2];
+    bool av[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int t = tw + 32 * i + r32;
+        av[i] = t < a.nt;
+        arow[i] = reinterpret_cast<const float *>(qb + (size_t)min(t, a.nt - 1) * a.q_nb2) + 4 * hh;
+        const int c = min(cw + 32 * i + r32, a.d_v - 1);
+        brow[i] = wb + (size_t)c * a.d_n + 4 * hh;
+    }
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const int np = a.d_n / 8;
+    f32x4 an[2], bn[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        an[i] = av[i] ? *reinterpret_cast<const f32x4 *>(arow[i]) : f32x4{0.f, 0.f, 0.f, 0.f};
+        bn[i] = *reinterpret_cast<const f32x4 *>(brow[i]);
+    }
+    for (int p = 0; p < np; ++p) {
+        const f32x4 ac[2] = {an[0], an[1]};
+        const f32x4 bc[2] = {bn[0], bn[1]};
+        if (p + 1 < np) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                an[i] = av[i] ? *reinterpret_cast<const f32x4 *>(arow[i] + 8 * (p + 1)) : f32x4{0.f, 0.f, 0.f, 0.f};
+                bn[i] = *reinterpret_cast<const f32x4 *>(brow[i] + 8 * (p + 1));
+            }
+        }
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ac[i][j4], bc[j][j4], acc[i][j], 0, 0, 0);
+    }
+    // C tile (i, j): lane column c = cw + 32 j + (lane & 31), rows t = tw + 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3)
+    char * db = reinterpret_cast<char *>(a.dst) + (size_t)h * a.d_nb1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = cw + 32 * j + r32;
+            if (c >= a.d_v) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = tw + 32 * i + 8 * (r >> 2) + 4 * hh + (r & 3);
+                if (t < a.nt) reinterpret_cast<float *>(db + (size_t)t * a.d_nb2)[c] = acc[i][j][r];
+            }
+        }
+}
+
 }  // namespace
 
 hipError_t launch_wkb_f32(const WkbArgs & a, hipStream_t stream) {
+    if (a.nt >= WKB_GEMM_MIN_TOKENS && a.d_n % 8 == 0) {
+        const dim3 grid((a.d_v + 127) / 128, (a.nt + 127) / 128, a.n_head);
+        hipLaunchKernelGGL(wkb_gemm_kernel, grid, dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
     const int total = a.n_head * a.d_v;
     if (a.d_n == 128) {
         const int rpb = 4 * (64 / 32) * WKB_NI;

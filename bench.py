@@ -278,17 +278,50 @@ def prefill_bench(args, inp) -> int:
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1000.0 / reps
+
+    def time_fn(fn, n=3):
+        fn()
+        torch.cuda.synchronize()
+        gg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gg):
+            fn()
+        gg.replay()
+        torch.cuda.synchronize()
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record()
+        for _ in range(n):
+            gg.replay()
+        a1.record()
+        torch.cuda.synchronize()
+        return a0.elapsed_time(a1) * 1000.0 / n
+
+    part = None
+    n_split = max(1, need // (((H + 31) // 32) * T * A.ops.part_floats(DV) * 4)) if need else 1
+    if n_split > 1:
+        part = torch.empty(((H + 31) // 32, T, n_split, A.ops.part_floats(DV)), dtype=torch.float32, device=dev)
+    us_wkb = time_fn(lambda: A.ggml_m4_wkb(wkb_w, qd[:, :, :I.D_NOPE], out=qcur[:, :, :DV]))
+    if part is not None:
+        us_attn = time_fn(lambda: A.ggml_m4_kqkv_partial(kc, qcur, mask, inp.kq_scale, n_split, part=part))
+        us_merge = time_fn(lambda: A.ggml_m4_phase_merge(part, out=out))
+    else:
+        us_attn = time_fn(lambda: A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws))
+        us_merge = 0.0
     live = (inp.mask == 0).sum(axis=1).astype(np.float64)          # keys visible to each token
     flop = float((2.0 * H * (DK + DV) * live).sum()) + 2.0 * H * DV * I.D_NOPE * T
     tf = flop / (us * 1e-6) / 1e12
+    flop_attn = float((2.0 * H * (DK + DV) * live).sum())
+    tf_attn = flop_attn / (us_attn * 1e-6) / 1e12
     rec = {"metric": "MLA chunked prefill (config 5): us/step and TFLOP/s of exact causal work", "value": round(us, 2),
            "unit": "us/step", "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": round(us / 1000.0, 4),
            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
            "config": {"workload": f"config 5: {T} tokens x {inp.n_kv} keys causal, 32 heads, f16 cache", "nt": T,
                       "n_kv": inp.n_kv},
            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
-                        "frac": round(tf / 2500.0, 4), "traffic": None, "gflop_per_step": round(flop / 1e9, 2)},
-           "cpu_baseline": None}
+                        "frac": round(tf / 2500.0, 4), "traffic": None, "gflop_per_step": round(flop / 1e9, 2),
+                        "attention_kernel": {"us": round(us_attn, 2), "tflops": round(tf_attn, 1),
+                                             "frac": round(tf_attn / 2500.0, 4), "splits": n_split}},
+           "cpu_baseline": None,
+           "extra": {"us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2), "us_phase_merge": round(us_merge, 2)}}
     print(json.dumps(rec), flush=True)
     return 0
 

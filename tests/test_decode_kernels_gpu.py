@@ -105,3 +105,48 @@ def test_short_and_long_kernels_agree_with_oracle(dev, dk, dv, n_kv, splits, sha
         ea, er, _ = errs(outs[a_], outs[b_])
         say(f"S={a_} vs S={b_}: max_abs={ea:.3e} max_rel={er:.3e}")
         assert ea <= 1e-2 and er <= (2e-2 if sharp else 3e-3)
+
+
+@pytest.mark.parametrize("dk,dv,n_kv,nt,splits", [
+    (576, 512, 3000, 6, (None, 1, 3)),      # a full 4-token group and a partial one
+    (320, 256, 2000, 9, (None, 2)),
+])
+@pytest.mark.parametrize("q_scale", [0.05, 1.0])
+def test_prefill_kernel_causal(dev, dk, dv, n_kv, nt, splits, q_scale):
+    """Several tokens (the prefill kernel: 4 tokens per workgroup, one per wave) with a causal
+    mask -- token t sees keys [0, n_kv - nt + t] -- against the oracle, with the library's split
+    count (None) and explicit ones."""
+    kc = I.randn(7300, n_kv * dk).astype(np.float16).reshape(n_kv, dk)
+    q = I.randn(7301, nt * 32 * dk, q_scale).reshape(nt, 32, dk)
+    mask = np.zeros((nt, n_kv), dtype=np.float32)
+    for t_ in range(nt):
+        mask[t_, n_kv - nt + t_ + 1:] = -np.inf
+    scale = float(np.float32(1.0 / np.sqrt(192.0)))
+    ref = orc.kqkv(kc, q, mask, scale, d_v=dv)
+    kc_d, q_d, m_d = (torch.from_numpy(x).to(dev) for x in (kc, q, mask))
+    for S in splits:
+        if S is None:
+            out = A.ggml_m4_kqkv(kc_d, q_d, m_d, scale)
+            torch.cuda.synchronize()
+            out = out.cpu().numpy()
+        else:
+            out = run_split(kc_d, q_d, m_d, scale, S, dv)
+        check(f"prefill {dk}/{dv} n_kv={n_kv} nt={nt} S={S} q_scale={q_scale} vs oracle", out, ref, 1e-2,
+              3e-3 if q_scale < 1 else 1e-2)
+
+
+@pytest.mark.parametrize("d_n,d_v", [(128, 512), (64, 256)])
+@pytest.mark.parametrize("nt", [1, 5, 16, 37, 130])
+def test_wkb_token_counts(dev, d_n, d_v, nt):
+    """WKB for one token (the HBM-streaming GEMV), a few (rows held while tokens stream) and many
+    (the f32-MFMA GEMM from 16 tokens on, with partial 128-token tiles), from a strided q view with
+    the engine's 192-float head stride, against the oracle at the f32 bar."""
+    H = 32
+    w = I.randn(7400, H * d_v * d_n).reshape(H, d_v, d_n)
+    qfull = I.randn(7401, nt * H * (d_n + 64)).reshape(nt, H, d_n + 64)
+    ref = orc.wkb(w, np.ascontiguousarray(qfull[:, :, :d_n]))
+    w_d = torch.from_numpy(w).to(dev)
+    q_d = torch.from_numpy(qfull).to(dev)
+    out = A.ggml_m4_wkb(w_d, q_d[:, :, :d_n])
+    torch.cuda.synchronize()
+    check(f"WKB d_n={d_n} D_v={d_v} nt={nt}", out.cpu().numpy(), ref, 1e-3, 1e-5)
