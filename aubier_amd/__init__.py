@@ -7,6 +7,12 @@ Python mirror of the op interface (aubier_amd.ops) and the seeded synthetic inpu
 """
 from .ops import (  # noqa: F401
     MlaM4Error,
+    Q8_0,
+    ggml_m4_phase_kvwrite,
+    ggml_m4_phase_wvb,
+    rope_params,
+    supports_phase_kvwrite,
+    supports_phase_wvb,
     default_splits,
     ggml_m4_kqkv,
     ggml_m4_kqkv_partial,

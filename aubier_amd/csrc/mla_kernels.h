@@ -56,7 +56,8 @@ hipError_t launch_merge(const char * part, int dv, int o_bytes, int n_split, int
 
 // WKB: dst[t][h][c] = sum_d w[h][c][d] * q[t][h][d]
 struct WkbArgs {
-    const float * w;        // contiguous [d_n, D_v, H]
+    const float * w;        // F32 W_kb, contiguous [d_n, D_v, H]
+    const uint8_t * wq;     // or Q8_0 W_kb: rows of d_n / 32 blocks of 34 bytes
     const float * q;        // q_nope
     int64_t q_nb1, q_nb2;
     float * dst;
@@ -64,5 +65,34 @@ struct WkbArgs {
     int d_n, d_v, n_head, nt;
 };
 hipError_t launch_wkb_f32(const WkbArgs & a, hipStream_t stream);
+hipError_t launch_wkb_q8(const WkbArgs & a, hipStream_t stream);     // d_n in {64, 128}
+
+// PHASE 1 (wv_b): dst[(o, t, h)] = Q8_0 w[h][o] . Q8_1(x[(:, t, h)])
+struct WvbArgs {
+    const uint8_t * w;      // Q8_0 rows [H][d_out] of d_in / 32 blocks
+    const float * x;        // element (i, t, h) at x + t x_nb1 + h x_nb2 (bytes) + 4 i
+    int64_t x_nb1, x_nb2;
+    float * dst;            // element (o, t, h) at dst + t d_nb1 + h d_nb2 + 4 o
+    int64_t d_nb1, d_nb2;
+    int d_in, d_out, n_head, nt;
+};
+hipError_t launch_wvb_q8(const WvbArgs & a, hipStream_t stream);     // d_in in {256, 512}
+
+// PHASE 0 (KV-write): gemv of cur through Q8_0 wkv_a [n_embd -> d_lat + n_rope], RMS norm of the
+// latent rows, YaRN rope of the last n_rope rows, dst = the row, cache row kidx[0] = f16(row).
+struct KvWriteArgs {
+    const float * cur;
+    const uint8_t * w;      // Q8_0 rows [d_lat + n_rope] of n_embd / 32 blocks
+    const float * nw;       // [d_lat]
+    void * kcache;          // F16 rows of kc_nb1 bytes
+    int64_t kc_nb1;
+    int64_t n_kv;
+    const int64_t * kidx;
+    const int32_t * pos;
+    float * dst;            // [d_lat + n_rope]
+    int n_embd, d_lat, n_rope;
+    float eps, theta_scale, freq_scale, ext_factor, attn_factor, corr0, corr1;
+};
+hipError_t launch_kvwrite(const KvWriteArgs & a, hipStream_t stream);  // n_embd in {4096, 7168}
 
 }  // namespace mla

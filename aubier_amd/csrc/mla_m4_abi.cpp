@@ -37,6 +37,19 @@ bool is_contiguous(const mla_m4_tensor * t) {
     return true;
 }
 
+// Q8_0 (ggml block_q8_0: f16 scale + 32 int8, 34 bytes): ne[0] a multiple of 32, nb[0] = the block
+// size, rows of ne[0] / 32 blocks packed, higher axes packed.
+constexpr size_t Q8_BLOCK = 34;
+bool is_q8_rows(const mla_m4_tensor * t) {
+    if (t->type != MLA_M4_TYPE_Q8_0 || t->ne[0] % 32 != 0 || t->nb[0] != Q8_BLOCK) return false;
+    size_t expect = Q8_BLOCK * (size_t)(t->ne[0] / 32);
+    for (int i = 1; i < 4; ++i) {
+        if (t->ne[i] != 1 && t->nb[i] != expect) return false;
+        expect *= (size_t)t->ne[i];
+    }
+    return true;
+}
+
 // ---------------------------------------------------------------- KQKV contract
 struct KqkvShape {
     int64_t dk, dv, n_kv, n_head, nt;
@@ -49,6 +62,7 @@ struct KqkvShape {
 // (graph planning); only type/ne/nb are checked, and a data pointer only when it is set.
 bool has_data(const mla_m4_tensor * t, bool plan) { return t && (plan || t->data); }
 bool al16(const void * p, bool plan) { return (plan && !p) || aligned16(p); }
+bool al4(const void * p, bool plan) { return (plan && !p) || (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 int check_kqkv(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_tensor * mask,
                const mla_m4_tensor * dst, KqkvShape * s, bool plan = false) {
@@ -176,12 +190,22 @@ int check_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, bool plan
 // ---------------------------------------------------------------- WKB contract
 int check_wkb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst, bool plan = false) {
     if (!has_data(w, plan) || !has_data(x, plan) || !has_data(dst, plan)) return MLA_M4_ERR_NULL;
-    if (w->type != MLA_M4_TYPE_F32 || x->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32)
+    if ((w->type != MLA_M4_TYPE_F32 && w->type != MLA_M4_TYPE_Q8_0) || x->type != MLA_M4_TYPE_F32 ||
+        dst->type != MLA_M4_TYPE_F32)
         return MLA_M4_ERR_TYPE;
     const int64_t dn = w->ne[0], dv = w->ne[1], nh = w->ne[2];
     if (dn < 1 || dv < 1 || nh < 1 || w->ne[3] != 1) return MLA_M4_ERR_SHAPE;
     if (x->ne[0] != dn || x->ne[1] != nh || x->ne[2] < 1 || x->ne[3] != 1) return MLA_M4_ERR_SHAPE;
     if (dst->ne[0] != dv || dst->ne[1] != nh || dst->ne[2] != x->ne[2] || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (w->type == MLA_M4_TYPE_Q8_0) {       // the reference's own form: rows of d_n / 32 blocks
+        if (!is_q8_rows(w) || !al4(w->data, plan)) return MLA_M4_ERR_STRIDE;
+        if (x->nb[0] != 4 || (x->nb[1] & 3u) || (x->nb[2] & 3u) || !al4(x->data, plan)) return MLA_M4_ERR_STRIDE;
+        if (dst->nb[0] != 4 || (dst->nb[1] & 3u) || (dst->nb[2] & 3u) || dst->nb[1] < (size_t)dv * 4)
+            return MLA_M4_ERR_STRIDE;
+        if (dn != 64 && dn != 128) return MLA_M4_ERR_UNSUPPORTED;
+        if (nh > 65535 || x->ne[2] > 65535) return MLA_M4_ERR_UNSUPPORTED;
+        return MLA_M4_OK;
+    }
     if (!is_contiguous(w) || !al16(w->data, plan)) return MLA_M4_ERR_STRIDE;
     if (x->nb[0] != 4 || (x->nb[1] & 15u) || (x->nb[2] & 15u) || !al16(x->data, plan)) return MLA_M4_ERR_STRIDE;
     if (dst->nb[0] != 4 || (dst->nb[1] & 3u) || (dst->nb[2] & 3u)) return MLA_M4_ERR_STRIDE;
@@ -189,6 +213,69 @@ int check_wkb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_ten
     if (dn != 64 && dn != 128) return MLA_M4_ERR_UNSUPPORTED;
     if (dv % 16 != 0 || nh * dv > INT32_MAX || x->ne[2] > INT32_MAX) return MLA_M4_ERR_UNSUPPORTED;
     return MLA_M4_OK;
+}
+
+// ---------------------------------------------------------------- PHASE 1 (wv_b) contract
+// w Q8_0 ne [d_in, d_out, H]; x F32 ne [d_in, nt, H] (the KQKV dst layout); dst F32 ne [d_out, nt, H]
+int check_wvb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst, bool plan = false) {
+    if (!has_data(w, plan) || !has_data(x, plan) || !has_data(dst, plan)) return MLA_M4_ERR_NULL;
+    if (w->type != MLA_M4_TYPE_Q8_0 || x->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
+    const int64_t din = w->ne[0], dout = w->ne[1], nh = w->ne[2];
+    if (din < 32 || dout < 1 || nh < 1 || w->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (x->ne[0] != din || x->ne[1] < 1 || x->ne[2] != nh || x->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (dst->ne[0] != dout || dst->ne[1] != x->ne[1] || dst->ne[2] != nh || dst->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (!is_q8_rows(w) || !al4(w->data, plan)) return MLA_M4_ERR_STRIDE;
+    if (x->nb[0] != 4 || (x->nb[1] & 3u) || (x->nb[2] & 3u) || !al4(x->data, plan)) return MLA_M4_ERR_STRIDE;
+    if (dst->nb[0] != 4 || (dst->nb[1] & 3u) || (dst->nb[2] & 3u) || !al4(dst->data, plan)) return MLA_M4_ERR_STRIDE;
+    if (din != 256 && din != 512) return MLA_M4_ERR_UNSUPPORTED;
+    if (x->ne[1] > 65535 || nh > 65535) return MLA_M4_ERR_UNSUPPORTED;
+    return MLA_M4_OK;
+}
+
+// ---------------------------------------------------------------- PHASE 0 (KV-write) contract
+// cur F32 ne [n_embd, 1]; wkv_a Q8_0 ne [n_embd, d_lat + n_dims]; kv_norm F32 ne [d_lat];
+// kcache F16 ne [d_lat + n_dims, n_kv] (rows of nb[1] bytes); kidx I64 ne [1]; pos I32 ne [1];
+// dst F32 ne [d_lat + n_dims]
+int check_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * w, const mla_m4_tensor * nw,
+                  const mla_m4_tensor * kc, const mla_m4_tensor * kidx, const mla_m4_tensor * pos,
+                  const mla_m4_rope_params * rp, const mla_m4_tensor * dst, bool plan = false) {
+    if (!has_data(cur, plan) || !has_data(w, plan) || !has_data(nw, plan) || !has_data(kc, plan) ||
+        !has_data(kidx, plan) || !has_data(pos, plan) || !has_data(dst, plan) || !rp)
+        return MLA_M4_ERR_NULL;
+    if (cur->type != MLA_M4_TYPE_F32 || w->type != MLA_M4_TYPE_Q8_0 || nw->type != MLA_M4_TYPE_F32 ||
+        kc->type != MLA_M4_TYPE_F16 || kidx->type != MLA_M4_TYPE_I64 || pos->type != MLA_M4_TYPE_I32 ||
+        dst->type != MLA_M4_TYPE_F32)
+        return MLA_M4_ERR_TYPE;
+    const int64_t n_embd = cur->ne[0], n_out = w->ne[1], n_dims = rp->n_dims, d_lat = n_out - n_dims;
+    if (cur->ne[1] != 1 || cur->ne[2] != 1 || cur->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (w->ne[0] != n_embd || w->ne[2] != 1 || w->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (n_dims < 2 || n_dims % 2 || d_lat < 32 || d_lat % 32 || nw->ne[0] != d_lat || nw->ne[1] != 1)
+        return MLA_M4_ERR_SHAPE;
+    if (kc->ne[0] != n_out || kc->ne[1] < 1 || kc->ne[2] != 1 || kc->ne[3] != 1) return MLA_M4_ERR_SHAPE;
+    if (kidx->ne[0] != 1 || pos->ne[0] != 1 || dst->ne[0] != n_out || dst->ne[1] != 1) return MLA_M4_ERR_SHAPE;
+    if (!is_q8_rows(w) || !al4(w->data, plan)) return MLA_M4_ERR_STRIDE;
+    if (!is_contiguous(cur) || !is_contiguous(nw) || !is_contiguous(dst) || !al4(cur->data, plan) ||
+        !al4(nw->data, plan) || !al4(dst->data, plan))
+        return MLA_M4_ERR_STRIDE;
+    if (kc->nb[0] != 2 || kc->nb[1] < (size_t)n_out * 2 || (kc->nb[1] & 1u)) return MLA_M4_ERR_STRIDE;
+    if (!(rp->freq_base > 0.0f) || !(rp->freq_scale > 0.0f) || !(rp->eps >= 0.0f) || rp->n_ctx_orig < 1 ||
+        !std::isfinite(rp->ext_factor) || !std::isfinite(rp->attn_factor) || !(rp->beta_fast > 0.0f) ||
+        !(rp->beta_slow > 0.0f))
+        return MLA_M4_ERR_ARG;
+    if ((n_embd != 4096 && n_embd != 7168) || n_out % 32 || n_out > 1024) return MLA_M4_ERR_UNSUPPORTED;
+    return MLA_M4_OK;
+}
+
+// YaRN correction dims (the host-side ggml_rope_yarn_corr_dims, vendor/llama.cpp/ggml/src/ggml.c:4632-4643)
+void rope_yarn_corr_dims(int n_dims, int n_ctx_orig, float freq_base, float beta_fast, float beta_slow, float dims[2]) {
+    const float pi = 3.14159265358979323846f;
+    auto corr_dim = [&](float n_rot) {
+        return (float)n_dims * logf((float)n_ctx_orig / (n_rot * 2.0f * pi)) / (2.0f * logf(freq_base));
+    };
+    const float start = floorf(corr_dim(beta_fast));
+    const float end = ceilf(corr_dim(beta_slow));
+    dims[0] = start > 0.0f ? start : 0.0f;
+    dims[1] = end < (float)(n_dims - 1) ? end : (float)(n_dims - 1);
 }
 
 }  // namespace
@@ -216,7 +303,9 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope, const mla_
     const int rc = check_wkb(w, q_nope, dst);
     if (rc != MLA_M4_OK) return rc;
     mla::WkbArgs a{};
-    a.w = static_cast<const float *>(w->data);
+    const bool q8 = w->type == MLA_M4_TYPE_Q8_0;
+    a.w = q8 ? nullptr : static_cast<const float *>(w->data);
+    a.wq = q8 ? static_cast<const uint8_t *>(w->data) : nullptr;
     a.q = static_cast<const float *>(q_nope->data);
     a.q_nb1 = (int64_t)q_nope->nb[1];
     a.q_nb2 = (int64_t)q_nope->nb[2];
@@ -227,7 +316,9 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope, const mla_
     a.d_v = (int)w->ne[1];
     a.n_head = (int)w->ne[2];
     a.nt = (int)q_nope->ne[2];
-    return mla::launch_wkb_f32(a, static_cast<hipStream_t>(stream)) == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+    const hipError_t e = q8 ? mla::launch_wkb_q8(a, static_cast<hipStream_t>(stream))
+                            : mla::launch_wkb_f32(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
 }
 
 size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * dst) {
@@ -319,7 +410,65 @@ int mla_m4_supports_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, 
 
 int mla_m4_supports_phase(int32_t phase, const mla_m4_tensor * src0, const mla_m4_tensor * dst) {
     if (phase == MLA_M4_PHASE_MERGE) return check_merge(src0, dst, true) == MLA_M4_OK;
-    return 0;   // phases 0 (KV-write) and 1 (wv_b) are not implemented by this library yet
+    return 0;   // phases 0 and 1 take more sources: mla_m4_supports_phase_kvwrite / _wvb
+}
+
+int mla_m4_phase_wvb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst, void * stream) {
+    const int rc = check_wvb(w, x, dst);
+    if (rc != MLA_M4_OK) return rc;
+    mla::WvbArgs a{};
+    a.w = static_cast<const uint8_t *>(w->data);
+    a.x = static_cast<const float *>(x->data);
+    a.x_nb1 = (int64_t)x->nb[1];
+    a.x_nb2 = (int64_t)x->nb[2];
+    a.dst = static_cast<float *>(dst->data);
+    a.d_nb1 = (int64_t)dst->nb[1];
+    a.d_nb2 = (int64_t)dst->nb[2];
+    a.d_in = (int)w->ne[0];
+    a.d_out = (int)w->ne[1];
+    a.n_head = (int)w->ne[2];
+    a.nt = (int)x->ne[1];
+    return mla::launch_wvb_q8(a, static_cast<hipStream_t>(stream)) == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
+int mla_m4_supports_phase_wvb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst) {
+    return check_wvb(w, x, dst, true) == MLA_M4_OK;
+}
+
+int mla_m4_phase_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * wkv_a, const mla_m4_tensor * kv_norm,
+                         const mla_m4_tensor * kcache, const mla_m4_tensor * kidx, const mla_m4_tensor * pos,
+                         const mla_m4_rope_params * rope, const mla_m4_tensor * dst, void * stream) {
+    const int rc = check_kvwrite(cur, wkv_a, kv_norm, kcache, kidx, pos, rope, dst);
+    if (rc != MLA_M4_OK) return rc;
+    mla::KvWriteArgs a{};
+    a.cur = static_cast<const float *>(cur->data);
+    a.w = static_cast<const uint8_t *>(wkv_a->data);
+    a.nw = static_cast<const float *>(kv_norm->data);
+    a.kcache = kcache->data;
+    a.kc_nb1 = (int64_t)kcache->nb[1];
+    a.n_kv = kcache->ne[1];
+    a.kidx = static_cast<const int64_t *>(kidx->data);
+    a.pos = static_cast<const int32_t *>(pos->data);
+    a.dst = static_cast<float *>(dst->data);
+    a.n_embd = (int)cur->ne[0];
+    a.n_rope = rope->n_dims;
+    a.d_lat = (int)wkv_a->ne[1] - rope->n_dims;
+    a.eps = rope->eps;
+    a.theta_scale = powf(rope->freq_base, -2.0f / (float)rope->n_dims);
+    a.freq_scale = rope->freq_scale;
+    a.ext_factor = rope->ext_factor;
+    a.attn_factor = rope->attn_factor;
+    float corr[2];
+    rope_yarn_corr_dims(rope->n_dims, rope->n_ctx_orig, rope->freq_base, rope->beta_fast, rope->beta_slow, corr);
+    a.corr0 = corr[0];
+    a.corr1 = corr[1];
+    return mla::launch_kvwrite(a, static_cast<hipStream_t>(stream)) == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
+int mla_m4_supports_phase_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * wkv_a, const mla_m4_tensor * kv_norm,
+                                  const mla_m4_tensor * kcache, const mla_m4_tensor * kidx, const mla_m4_tensor * pos,
+                                  const mla_m4_rope_params * rope, const mla_m4_tensor * dst) {
+    return check_kvwrite(cur, wkv_a, kv_norm, kcache, kidx, pos, rope, dst, true) == MLA_M4_OK;
 }
 
 int mla_m4_resolve_flag(int flag, int gpu_core) {

@@ -69,6 +69,12 @@ class MlaTensor(ctypes.Structure):
     ]
 
 
+class RopeParams(ctypes.Structure):
+    """mla_m4_rope_params: op_params[1..9] of ggml_m4_phase_kvwrite."""
+    _fields_ = [(n, ctypes.c_float) for n in ("freq_base", "freq_scale", "ext_factor", "attn_factor", "beta_fast",
+                                               "beta_slow", "eps")] + [("n_dims", ctypes.c_int32), ("n_ctx_orig", ctypes.c_int32)]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 _EXPORTS = {
@@ -86,6 +92,12 @@ _EXPORTS = {
     "mla_m4_supports_kqkv": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 4),
     "mla_m4_supports_phase": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(MlaTensor), ctypes.POINTER(MlaTensor)]),
     "mla_m4_resolve_flag": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
+    "mla_m4_phase_wvb": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_void_p]),
+    "mla_m4_supports_phase_wvb": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3),
+    "mla_m4_phase_kvwrite": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 6 + [ctypes.POINTER(RopeParams),
+                                                                              ctypes.POINTER(MlaTensor), ctypes.c_void_p]),
+    "mla_m4_supports_phase_kvwrite": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 6 + [ctypes.POINTER(RopeParams),
+                                                                                       ctypes.POINTER(MlaTensor)]),
 }
 
 
@@ -110,13 +122,51 @@ def exported_symbols() -> list[str]:
 
 
 # ------------------------------------------------------------------------------------ views
-_DT = {torch.float32: (TYPE_F32, 4), torch.float16: (TYPE_F16, 2)}
+TYPE_Q8_0, TYPE_I32, TYPE_I64 = 8, 26, 27
+_DT = {torch.float32: (TYPE_F32, 4), torch.float16: (TYPE_F16, 2), torch.int32: (TYPE_I32, 4),
+       torch.int64: (TYPE_I64, 8)}
 
 
-def view(t: Optional[torch.Tensor]) -> Optional[MlaTensor]:
+class Q8_0:
+    """A Q8_0 tensor (ggml block_q8_0: f16 scale + 32 int8 = 34 bytes per 32 elements): `blocks`
+    is a uint8 tensor [..., ne0 / 32 * 34] of packed rows; the ggml shape is (ne0, reversed leading
+    dims of `blocks`)."""
+
+    def __init__(self, blocks: torch.Tensor, ne0: int):
+        assert blocks.dtype == torch.uint8 and blocks.is_contiguous() and ne0 % 32 == 0
+        assert blocks.shape[-1] == ne0 // 32 * 34
+        self.blocks, self.ne0 = blocks, ne0
+
+    @property
+    def device(self):
+        return self.blocks.device
+
+
+def _view_q8(t: Q8_0) -> MlaTensor:
+    v = MlaTensor()
+    v.data = t.blocks.data_ptr()
+    v.type = TYPE_Q8_0
+    rows = list(reversed(t.blocks.shape[:-1]))
+    shape = [t.ne0] + rows
+    nb = [34, t.blocks.shape[-1]]
+    for r in rows[:-1] if rows else []:
+        nb.append(nb[-1] * r)
+    while len(shape) < 4:
+        shape.append(1)
+    while len(nb) < 4:
+        nb.append(nb[-1] * shape[len(nb) - 1])
+    for i in range(4):
+        v.ne[i] = int(shape[i])
+        v.nb[i] = int(nb[i])
+    return v
+
+
+def view(t) -> Optional[MlaTensor]:
     """ggml-style view of a torch tensor: ne/nb are the reversed shape/strides (bytes)."""
     if t is None:
         return None
+    if isinstance(t, Q8_0):
+        return _view_q8(t)
     if t.dtype not in _DT:
         raise MlaM4Error("view", -2)
     if t.dim() > 4:
@@ -150,14 +200,16 @@ def _check(op: str, rc: int) -> None:
 
 
 # ------------------------------------------------------------------------------------ ops
-def ggml_m4_wkb(w_kb: torch.Tensor, q_nope: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """GGML_OP_M4_WKB: out[t, h, c] = sum_d w_kb[h, c, d] * q_nope[t, h, d] (f32).
+def ggml_m4_wkb(w_kb, q_nope: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GGML_OP_M4_WKB: out[t, h, c] = sum_d w_kb[h, c, d] * q_nope[t, h, d].
 
-    w_kb [H, D_v, d_n] contiguous; q_nope [nt, H, d_n] (strided view ok); out [nt, H, D_v]
-    (a view into the Qcur buffer ok)."""
+    w_kb f32 [H, D_v, d_n] contiguous, or a Q8_0 with blocks [H, D_v, d_n / 32 * 34] (the
+    reference's form: Q8_1 activation numerics); q_nope [nt, H, d_n] (strided view ok);
+    out [nt, H, D_v] (a view into the Qcur buffer ok)."""
     lib = load_library()
     if out is None:
-        out = torch.empty((q_nope.shape[0], w_kb.shape[0], w_kb.shape[1]), dtype=torch.float32, device=q_nope.device)
+        H, D_v = (w_kb.blocks.shape[0], w_kb.blocks.shape[1]) if isinstance(w_kb, Q8_0) else (w_kb.shape[0], w_kb.shape[1])
+        out = torch.empty((q_nope.shape[0], H, D_v), dtype=torch.float32, device=q_nope.device)
     vw, vq, vo = view(w_kb), view(q_nope), view(out)
     _check("ggml_m4_wkb", lib.mla_m4_wkb(_ptr(vw), _ptr(vq), _ptr(vo), _stream(q_nope)))
     return out
@@ -262,3 +314,47 @@ def resolve_flag(flag: int, gpu_core: bool) -> bool:
 
 def kq_scale_default(d_k_nope: int = 128, d_rope: int = 64) -> float:
     return 1.0 / math.sqrt(d_k_nope + d_rope)
+
+
+# ---------------------------------------------------------------- PHASE 0 / 1 (reference geometry)
+def ggml_m4_phase_wvb(w: Q8_0, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GGML_OP_M4_PHASE phase 1 (wv_b): w Q8_0 blocks [H, d_out, d_in / 32 * 34]; x f32 [H, nt, d_in]
+    (the KQKV output layout) -> out [H, nt, d_out]."""
+    lib = load_library()
+    if out is None:
+        out = torch.empty((x.shape[0], x.shape[1], w.blocks.shape[1]), dtype=torch.float32, device=x.device)
+    _check("ggml_m4_phase_wvb", lib.mla_m4_phase_wvb(_ptr(view(w)), _ptr(view(x)), _ptr(view(out)), _stream(x)))
+    return out
+
+
+def rope_params(**kw) -> RopeParams:
+    rp = RopeParams()
+    for k, v in kw.items():
+        setattr(rp, k, v)
+    return rp
+
+
+def ggml_m4_phase_kvwrite(cur: torch.Tensor, wkv_a: Q8_0, kv_norm: torch.Tensor, kcache: torch.Tensor,
+                          kidx: torch.Tensor, pos: torch.Tensor, rope: RopeParams,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GGML_OP_M4_PHASE phase 0 (KV-write): cur f32 [n_embd]; wkv_a Q8_0 blocks [n_out, n_embd/32*34];
+    kv_norm f32 [d_lat]; kcache f16 [n_kv, n_out] (row kidx[0] written in place); kidx int64 [1];
+    pos int32 [1] -> Kcur f32 [n_out]."""
+    lib = load_library()
+    if out is None:
+        out = torch.empty((wkv_a.blocks.shape[0],), dtype=torch.float32, device=cur.device)
+    _check("ggml_m4_phase_kvwrite",
+           lib.mla_m4_phase_kvwrite(_ptr(view(cur)), _ptr(view(wkv_a)), _ptr(view(kv_norm)), _ptr(view(kcache)),
+                                    _ptr(view(kidx)), _ptr(view(pos)), ctypes.byref(rope), _ptr(view(out)),
+                                    _stream(cur)))
+    return out
+
+
+def supports_phase_wvb(w, x, out) -> bool:
+    return bool(load_library().mla_m4_supports_phase_wvb(_ptr(view(w)), _ptr(view(x)), _ptr(view(out))))
+
+
+def supports_phase_kvwrite(cur, wkv_a, kv_norm, kcache, kidx, pos, rope: RopeParams, out) -> bool:
+    return bool(load_library().mla_m4_supports_phase_kvwrite(_ptr(view(cur)), _ptr(view(wkv_a)), _ptr(view(kv_norm)),
+                                                             _ptr(view(kcache)), _ptr(view(kidx)), _ptr(view(pos)),
+                                                             ctypes.byref(rope), _ptr(view(out))))

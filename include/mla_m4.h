@@ -60,7 +60,7 @@ typedef struct mla_m4_tensor {
 } mla_m4_tensor;
 
 /* GGML_OP_M4_PHASE selectors (op_params[0]).  0 and 1 keep the reference's meaning
- * (patches/ggml-m4/m4-phase.cuh:3-14); 2 is the split-K merge. */
+ * (patches/ggml-m4/m4-phase.cuh:3-14): KV-write and wv_b; 2 is the split-K merge. */
 enum {
     MLA_M4_PHASE_KVWRITE = 0,
     MLA_M4_PHASE_WVB     = 1,
@@ -90,11 +90,17 @@ const char * mla_m4_status_str(int status);
  * GGML_OP_M4_WKB -- the MLA absorption of the query's nope half into the latent space.
  * Replaces ggml_cuda_m4_wkb (patches/ggml-m4/m4-wkb.cu:71-86); builder contract ggml_m4_wkb
  * (vendor/llama.cpp/ggml/src/ggml.c:3405-3426), generalised from the fixed Q8_0 [64,256,32]:
- *   w      F32  ne [d_n, D_v, H]     contiguous (W_kb: W[h][c][d])
- *   q_nope F32  ne [d_n, H, nt]      nb[0] = 4, any 16-byte-aligned head/token strides
- *                                     (the engine's view of q with a (d_n + d_r)-float head stride)
+ *   w      F32  ne [d_n, D_v, H]     contiguous (W_kb: W[h][c][d]), d_n in {64, 128}
+ *          or Q8_0 ne [d_n, D_v, H]  rows of d_n / 32 blocks (nb[0] = 34), 4-byte aligned --
+ *                                     the reference's own form
+ *   q_nope F32  ne [d_n, H, nt]      nb[0] = 4, any 16-byte-aligned (4-byte for Q8_0) head/token
+ *                                     strides (the engine's view of q with a (d_n + d_r)-float
+ *                                     head stride)
  *   dst    F32  ne [D_v, H, nt]      nb[0] = 4, 16-byte-aligned strides (may be a view into Qcur)
- *   dst[t][h][c] = sum_d w[h][c][d] * q_nope[t][h][d]          (f32 throughout, as ggml-cpu)
+ *   F32:  dst[t][h][c] = sum_d w[h][c][d] * q_nope[t][h][d]         (f32 throughout, as ggml-cpu)
+ *   Q8_0: the reference kernel's numerics (m4-wkb.cu:21-53): per 32-block b the activation is
+ *         quantised to int8 with q = roundf(x / d), d = amax / 127 stored as f16 (d16), and
+ *         dst = sum_b fma(wd_b * d16_b, (float) sum_k qw * qx, .) over the blocks in order.
  * ------------------------------------------------------------------------------------------- */
 int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
                const mla_m4_tensor * dst, void * stream);
@@ -150,6 +156,51 @@ int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
 int mla_m4_phase_merge(const mla_m4_tensor * part, const mla_m4_tensor * dst, void * stream);
 
 /* -------------------------------------------------------------------------------------------
+ * GGML_OP_M4_PHASE, phase MLA_M4_PHASE_WVB -- the MLA value absorption (kqv_mla): replaces the
+ * phase-1 branch of ggml_cuda_m4_phase (patches/ggml-m4/m4-phase.cu:52-88, 209-224); builder
+ * ggml_m4_phase_wvb (vendor/llama.cpp/ggml/src/ggml.c:3520-3539), generalised from [256,128,32]:
+ *   w    Q8_0 ne [d_in, d_out, H]   rows of d_in / 32 blocks, d_in in {256, 512}
+ *   x    F32  ne [d_in, nt, H]      nb[0] = 4 (the KQKV output), 4-byte-aligned strides
+ *   dst  F32  ne [d_out, nt, H]     nb[0] = 4
+ * Numerics of the reference kernel: x quantised per 32-block (id = 1 / d, q = roundf(x * id),
+ * f16 scale); lane k of 32 accumulates fma(wd_b * xd_b, qw[b][k] * qx[b][k], .) over the blocks
+ * in order, then the xor butterfly 16, 8, 4, 2, 1 of warp_reduce_sum.
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_phase_wvb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst,
+                     void * stream);
+
+/* The rope / norm scalars of phase 0, op_params[1..9] of ggml_m4_phase_kvwrite in order
+ * (ggml.c:3462-3468: an int32 array, f32 values bit-cast). */
+typedef struct mla_m4_rope_params {
+    float   freq_base, freq_scale, ext_factor, attn_factor, beta_fast, beta_slow;
+    float   eps;
+    int32_t n_dims, n_ctx_orig;
+} mla_m4_rope_params;
+
+/* -------------------------------------------------------------------------------------------
+ * GGML_OP_M4_PHASE, phase MLA_M4_PHASE_KVWRITE -- the step that writes the row KQKV streams:
+ * replaces the phase-0 branch of ggml_cuda_m4_phase (patches/ggml-m4/m4-phase.cu:95-200, 226-273);
+ * builder ggml_m4_phase_kvwrite (ggml.c:3469-3517), generalised from 4096 -> 256 + 64:
+ *   cur     F32  ne [n_embd, 1]               the attn_norm output, n_embd in {4096, 7168}
+ *   wkv_a   Q8_0 ne [n_embd, d_lat + n_dims]  rows of n_embd / 32 blocks
+ *   kv_norm F32  ne [d_lat]                   attn_kv_a_norm weight
+ *   kcache  F16  ne [d_lat + n_dims, n_kv]    WRITTEN IN PLACE at row kidx[0] (as ggml_set_rows)
+ *   kidx    I64  ne [1], pos I32 ne [1]       read on the device (no host read of device memory);
+ *                                             a row outside [0, n_kv) is not written
+ *   dst     F32  ne [d_lat + n_dims]          Kcur: the values the cache row received
+ * Two launches: the gemv (the reference's Q8_1 numerics: per input block q = roundf(x * (1/d)),
+ * (wd * d16) * sum, butterfly per 32 blocks, partials in order), then one workgroup that
+ * RMS-norms rows [0, d_lat) (1 / sqrt(mean of squares + eps) * kv_norm), ropes rows
+ * [d_lat, d_lat + n_dims) (NORMAL mode, YaRN: theta = pos * theta_scale^p with the ramp mix when
+ * ext_factor != 0, cos / sin scaled by attn_factor (1 + 0.1 ln(1 / freq_scale))), and scatters.
+ * n_dims even, d_lat a multiple of 32, d_lat + n_dims <= 1024.
+ * ------------------------------------------------------------------------------------------- */
+int mla_m4_phase_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * wkv_a,
+                         const mla_m4_tensor * kv_norm, const mla_m4_tensor * kcache,
+                         const mla_m4_tensor * kidx, const mla_m4_tensor * pos,
+                         const mla_m4_rope_params * rope, const mla_m4_tensor * dst, void * stream);
+
+/* -------------------------------------------------------------------------------------------
  * supports_op mirrors (ggml-cuda.cu:5848-5885): 1 if the entry point above accepts these
  * tensors, 0 otherwise.  They run the same host-side contract checks as the launch, without
  * launching, so the backend's supports_op and the launcher cannot disagree.  Data pointers may
@@ -162,6 +213,13 @@ int mla_m4_supports_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
 int mla_m4_supports_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
                          const mla_m4_tensor * mask, const mla_m4_tensor * dst);
 int mla_m4_supports_phase(int32_t phase, const mla_m4_tensor * src0, const mla_m4_tensor * dst);
+/* phases 0 and 1 take more sources than (src0, dst): their own mirrors (mla_m4_supports_phase
+ * returns 0 for them) */
+int mla_m4_supports_phase_wvb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_tensor * dst);
+int mla_m4_supports_phase_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * wkv_a,
+                                  const mla_m4_tensor * kv_norm, const mla_m4_tensor * kcache,
+                                  const mla_m4_tensor * kidx, const mla_m4_tensor * pos,
+                                  const mla_m4_rope_params * rope, const mla_m4_tensor * dst);
 
 /* -------------------------------------------------------------------------------------------
  * The tri-state enable flag of each op (engine/m1_session.h:152-166, resolved at

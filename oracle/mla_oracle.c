@@ -490,3 +490,225 @@ void orc_kqkv_bench_pattern(int64_t n_k, uint16_t *kc, int64_t n_q, float *q) {
 }
 
 int orc_max_threads(void) { return omp_get_max_threads(); }
+
+/* ------------------------------------------------------------------ Q8_0 x Q8_1 paths
+ * The reference geometry's quantised ops follow the GPU MMVQ numerics (not ggml-cpu's Q8_0.Q8_0
+ * mul_mat): the f32 activation is quantised per 32-value block to int8 with an f16 scale, the
+ * block dot is an exact int32 sum, and the f32 result accumulates wd * d16 * sum.  The
+ * restatements below keep the reference kernels' operation order: the floating steps are written
+ * with explicit fmaf/fmaxf so the C compiler cannot contract or reassociate them (nvcc contracts
+ * `acc += wd * d16 * (float)sum` into fma(wd * d16, sum, acc); wd * d16 is exact in f32, both
+ * being f16 values).
+ *
+ * Q8_0 block (ggml block_q8_0): f16 d, then 32 int8 qs -- 34 bytes, rows of ne0 / 32 blocks. */
+
+static inline float q8_scale(const uint8_t *blk) { uint16_t h; memcpy(&h, blk, 2); return f16_to_f32(h); }
+
+/* Activation block quantisation, the WKB form (patches/ggml-m4/m4-wkb.cu:36-47):
+ * d = amax / 127, d16 = f16(d), q = roundf(x / d) (0 when amax == 0). */
+static void quant_block_div(const float *x, int8_t *q, float *d16) {
+    float amax = 0.0f;
+    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(x[k]));
+    const float d = amax / 127.0f;
+    *d16 = f16_to_f32(f32_to_f16_rne(d));
+    for (int k = 0; k < 32; ++k) q[k] = (int8_t)(amax == 0.0f ? 0 : (int)roundf(x[k] / d));
+}
+
+/* The PHASE form (patches/ggml-m4/m4-phase.cu:58-66, 106-111, quantize_q8_1's): id = d ? 1/d : 0,
+ * q = roundf(x * id). */
+static void quant_block_mul(const float *x, int8_t *q, float *d16) {
+    float amax = 0.0f;
+    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(x[k]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    *d16 = f16_to_f32(f32_to_f16_rne(d));
+    for (int k = 0; k < 32; ++k) q[k] = (int8_t)(int)roundf(x[k] * id);
+}
+
+static inline int32_t dot_q8(const int8_t *a, const int8_t *b) {
+    int32_t s = 0;
+    for (int k = 0; k < 32; ++k) s += (int32_t)a[k] * (int32_t)b[k];
+    return s;
+}
+
+/* The 32-lane butterfly of ggml-cuda's warp_reduce_sum (xor 16, 8, 4, 2, 1), value of lane 0. */
+static float warp32_sum(const float *v_in) {
+    float v[32], t[32];
+    memcpy(v, v_in, sizeof v);
+    for (int off = 16; off > 0; off >>= 1) {
+        for (int k = 0; k < 32; ++k) t[k] = v[k] + v[k ^ off];
+        memcpy(v, t, sizeof v);
+    }
+    return v[0];
+}
+
+/* GGML_OP_M4_WKB with a Q8_0 W_kb (patches/ggml-m4/m4-wkb.cu:21-69), generalised to d_n = 32 nb
+ * and nt tokens: out[t][h][c] = sum_b fma(wd_b * xd_b, sum_b, .) over the row's blocks in order.
+ * w: [n_head][d_v] rows of d_n / 32 blocks; q: f32, element (t, h, d) at q + t q_nb2 + h q_nb1
+ * (bytes) + 4 d; out: element (t, h, c) at out + t d_nb2 + h d_nb1 + 4 c. */
+int orc_wkb_q8(const uint8_t *w, int64_t d_n, int64_t d_v, int64_t n_head, const float *q, int64_t nt,
+               int64_t q_nb1, int64_t q_nb2, float *out, int64_t d_nb1, int64_t d_nb2, int mutant) {
+    if (d_n % 32 != 0 || d_n > 1024) return -1;
+    const int64_t nb = d_n / 32;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t t = 0; t < nt; ++t)
+        for (int64_t h = 0; h < n_head; ++h) {
+            int8_t xq[1024];
+            float xd[32];
+            const float *x = (const float *)((const char *)q + t * q_nb2 + h * q_nb1);
+            for (int64_t b = 0; b < nb; ++b) {
+                if (mutant == 1) quant_block_mul(x + 32 * b, xq + 32 * b, &xd[b]);   /* wrong form */
+                else quant_block_div(x + 32 * b, xq + 32 * b, &xd[b]);
+            }
+            float *o = (float *)((char *)out + t * d_nb2 + h * d_nb1);
+            for (int64_t c = 0; c < d_v; ++c) {
+                const uint8_t *row = w + (h * d_v + c) * nb * 34;
+                float acc = 0.0f;
+                for (int64_t b = 0; b < nb; ++b) {
+                    const uint8_t *blk = row + (mutant == 2 ? 34 * ((b + 1) % nb) : 34 * b);   /* block mix-up */
+                    const int32_t s = dot_q8((const int8_t *)(blk + 2), xq + 32 * b);
+                    acc = fmaf(q8_scale(blk) * xd[b], (float)s, acc);
+                }
+                o[c] = acc;
+            }
+        }
+    return 0;
+}
+
+/* GGML_OP_M4_PHASE phase 1, wv_b (patches/ggml-m4/m4-phase.cu:52-88), generalised to d_in = 32 nb
+ * inputs per head and nt tokens: per (token, head, output) the 32 lanes' partials
+ * p_k = sum_b fma(wd_b * xd_b, q_w[b][k] * q_x[b][k], .) (blocks in order), then the butterfly.
+ * w: [n_head][d_out] rows of d_in / 32 blocks; x: (t, h, i) at x + t x_nb2 + h x_nb1 + 4 i;
+ * out: (t, h, o) at out + t o_nb2 + h o_nb1 + 4 o. */
+int orc_wvb_q8(const uint8_t *w, int64_t d_in, int64_t d_out, int64_t n_head, const float *x, int64_t nt,
+               int64_t x_nb1, int64_t x_nb2, float *out, int64_t o_nb1, int64_t o_nb2, int mutant) {
+    if (d_in % 32 != 0 || d_in > 1024) return -1;
+    const int64_t nb = d_in / 32;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t t = 0; t < nt; ++t)
+        for (int64_t h = 0; h < n_head; ++h) {
+            int8_t xq[1024];
+            float xd[32];
+            const float *xh = (const float *)((const char *)x + t * x_nb2 + h * x_nb1);
+            for (int64_t b = 0; b < nb; ++b) {
+                if (mutant == 1) quant_block_div(xh + 32 * b, xq + 32 * b, &xd[b]);   /* wrong form */
+                else quant_block_mul(xh + 32 * b, xq + 32 * b, &xd[b]);
+            }
+            float *o = (float *)((char *)out + t * o_nb2 + h * o_nb1);
+            for (int64_t r = 0; r < d_out; ++r) {
+                const uint8_t *row = w + (h * d_out + r) * nb * 34;
+                float p[32];
+                for (int k = 0; k < 32; ++k) {
+                    float acc = 0.0f;
+                    for (int64_t b = 0; b < nb; ++b) {
+                        const uint8_t *blk = row + 34 * b;
+                        const int32_t qq = (int32_t)((const int8_t *)(blk + 2))[k] * (int32_t)xq[32 * b + k];
+                        acc = fmaf(q8_scale(blk) * xd[b], (float)qq, acc);
+                    }
+                    p[k] = acc;
+                }
+                float s = 0.0f;
+                if (mutant == 2) { for (int k = 0; k < 32; ++k) s += p[k]; }   /* serial, not the butterfly */
+                else s = warp32_sum(p);
+                o[r] = s;
+            }
+        }
+    return 0;
+}
+
+/* YaRN correction dims (vendor/llama.cpp/ggml/src/ggml.c:4632-4643). */
+void orc_rope_yarn_corr_dims(int n_dims, int n_ctx_orig, float freq_base, float beta_fast, float beta_slow, float dims[2]) {
+    const float pi = 3.14159265358979323846f;
+    const float cf = (float)n_dims * logf((float)n_ctx_orig / (beta_fast * 2.0f * pi)) / (2.0f * logf(freq_base));
+    const float cs = (float)n_dims * logf((float)n_ctx_orig / (beta_slow * 2.0f * pi)) / (2.0f * logf(freq_base));
+    const float start = floorf(cf), end = ceilf(cs);
+    dims[0] = start > 0.0f ? start : 0.0f;
+    dims[1] = end < (float)(n_dims - 1) ? end : (float)(n_dims - 1);
+}
+
+/* GGML_OP_M4_PHASE phase 0, KV-write (patches/ggml-m4/m4-phase.cu:95-200), generalised to
+ * n_embd = 1024 nw inputs and d_lat + n_rope outputs (reference: 4096 -> 256 + 64):
+ *  1. gemv: out[o] = per 32-block b: wd d16 sum (plain products, d16 and q from the PHASE form of
+ *     the block quantisation); the blocks of a warp (32 consecutive) reduced by the butterfly,
+ *     then the warp partials summed in order;
+ *  2. rms norm of rows [0, d_lat): squares reduced per 32 rows by the butterfly, the partials of
+ *     all (d_lat + n_rope) / 32 warps summed in order, scale = 1 / sqrt(s / d_lat + eps),
+ *     kcur = scale * v * nw;
+ *  3. rope of rows [d_lat, d_lat + n_rope), pairs p: theta_e = pos * theta_scale^p, theta =
+ *     freq_scale theta_e mixed with theta_e by the YaRN ramp when ext_factor != 0, mscale =
+ *     attn_factor (1 + 0.1 ln(1 / freq_scale)) then, (x0, x1) rotated by theta and scaled;
+ *  4. the row as f16 into kcache row kidx (round to nearest even); dst = kcur (f32).
+ * The CUDA math of steps 2-3 (rsqrtf, powf, cosf, sinf, logf) is restated with the C library's
+ * f32 functions: the GPU result differs by its own math library's ulps, which grow with pos
+ * for the rope (documented in the test tolerances). */
+int orc_kvwrite(const float *cur, int64_t n_embd, const uint8_t *w, int64_t d_lat, int64_t n_rope, const float *nw,
+                uint16_t *kcache, int64_t kc_nb1, int64_t kidx, int32_t pos,
+                float freq_base, float freq_scale, float ext_factor, float attn_factor, float beta_fast,
+                float beta_slow, float eps, int32_t n_ctx_orig, float *dst, int mutant) {
+    const int64_t n_out = d_lat + n_rope;
+    const int64_t nb = n_embd / 32;
+    if (n_embd % 1024 != 0 || n_out % 32 != 0 || d_lat % 32 != 0 || n_rope % 2 != 0 || n_rope > 2 * n_out) return -1;
+    const int n_warps = (int)(nb / 32);
+    float *kcur = (float *)malloc((size_t)n_out * sizeof(float));
+    int8_t *xq = (int8_t *)malloc((size_t)n_embd);
+    float *xd = (float *)malloc((size_t)nb * sizeof(float));
+    if (!kcur || !xq || !xd) { free(kcur); free(xq); free(xd); return -2; }
+    for (int64_t b = 0; b < nb; ++b) quant_block_mul(cur + 32 * b, xq + 32 * b, &xd[b]);
+    /* 1. gemv */
+    for (int64_t o = 0; o < n_out; ++o) {
+        const uint8_t *row = w + o * nb * 34;
+        float total = 0.0f;
+        for (int wv = 0; wv < n_warps; ++wv) {
+            float p[32];
+            for (int k = 0; k < 32; ++k) {
+                const int64_t b = 32 * wv + k;
+                const uint8_t *blk = row + 34 * b;
+                const int32_t s = dot_q8((const int8_t *)(blk + 2), xq + 32 * b);
+                p[k] = (q8_scale(blk) * xd[b]) * (float)s;
+            }
+            const float ws = warp32_sum(p);
+            total = (wv == 0) ? ws : total + ws;
+        }
+        kcur[o] = total;
+    }
+    /* 2. rms norm over [0, d_lat) */
+    float s = 0.0f;
+    for (int64_t wv = 0; wv < n_out / 32; ++wv) {
+        float p[32];
+        for (int k = 0; k < 32; ++k) {
+            const int64_t r = 32 * wv + k;
+            const float v = r < d_lat ? kcur[r] : 0.0f;
+            p[k] = v * v;
+        }
+        s += warp32_sum(p);
+    }
+    const float scale = 1.0f / sqrtf(s / (float)d_lat + eps);
+    /* 3. rope over [d_lat, d_lat + n_rope) */
+    float corr[2];
+    orc_rope_yarn_corr_dims((int)n_rope, n_ctx_orig, freq_base, beta_fast, beta_slow, corr);
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_rope);
+    for (int64_t p = 0; p < n_rope / 2; ++p) {
+        const float x0 = kcur[d_lat + 2 * p], x1 = kcur[d_lat + 2 * p + 1];
+        const float theta_extrap = (float)pos * powf(theta_scale, (float)p);
+        float mscale = attn_factor;
+        float theta = freq_scale * theta_extrap;
+        if (ext_factor != 0.0f) {
+            const float y = ((float)p - corr[0]) / fmaxf(0.001f, corr[1] - corr[0]);
+            const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * ext_factor;
+            theta = theta * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+            mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
+        }
+        const float co = cosf(theta) * mscale, si = sinf(theta) * mscale;
+        kcur[d_lat + 2 * p] = x0 * co - x1 * si;
+        kcur[d_lat + 2 * p + 1] = (mutant == 1 ? -x0 : x0) * si + x1 * co;    /* sign slip */
+    }
+    for (int64_t r = 0; r < d_lat; ++r) kcur[r] = scale * kcur[r] * nw[r];
+    /* 4. the cache row and dst */
+    uint16_t *crow = (uint16_t *)((char *)kcache + (mutant == 2 ? kidx + 1 : kidx) * kc_nb1);   /* wrong row */
+    for (int64_t r = 0; r < n_out; ++r) {
+        crow[r] = f32_to_f16_rne(kcur[r]);
+        dst[r] = kcur[r];
+    }
+    free(kcur); free(xq); free(xd);
+    return 0;
+}

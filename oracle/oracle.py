@@ -49,6 +49,15 @@ def lib() -> ctypes.CDLL:
         L.orc_wkb.argtypes = [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_int, ctypes.c_int]
         L.orc_wkb.restype = ctypes.c_int
         L.orc_kqkv_bench_pattern.argtypes = [_I64, _P, _I64, _P]
+        L.orc_wkb_q8.argtypes = [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_int]
+        L.orc_wkb_q8.restype = ctypes.c_int
+        L.orc_wvb_q8.argtypes = [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_int]
+        L.orc_wvb_q8.restype = ctypes.c_int
+        L.orc_rope_yarn_corr_dims.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                              ctypes.c_float, _P]
+        L.orc_kvwrite.argtypes = [_P, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _I32] + [ctypes.c_float] * 7 + \
+            [_I32, _P, ctypes.c_int]
+        L.orc_kvwrite.restype = ctypes.c_int
         L.orc_max_threads.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -192,3 +201,73 @@ def mla_step(inp, threads: Optional[int] = None) -> tuple[np.ndarray, np.ndarray
 
 
 os.environ.setdefault("OMP_WAIT_POLICY", "PASSIVE")
+
+
+# ---------------------------------------------------------------- Q8_0 x Q8_1 (reference geometry)
+def q8_0_random(seed: int, rows: int, ne0: int, scale: float = 0.01) -> np.ndarray:
+    """Random Q8_0 rows as raw bytes [rows, ne0 / 32 * 34]: int8 qs in [-127, 127] and positive f16
+    scales (any valid Q8_0 bytes do; ggml's own quantiser is not needed to test the dot)."""
+    nb = ne0 // 32
+    r = np.random.default_rng(seed)
+    qs = r.integers(-127, 128, size=(rows, nb, 32), dtype=np.int64).astype(np.int8)
+    d = (np.abs(r.standard_normal((rows, nb))) * scale + scale / 8).astype(np.float16)
+    out = np.empty((rows, nb, 34), dtype=np.uint8)
+    out[:, :, :2] = d.view(np.uint8).reshape(rows, nb, 2)
+    out[:, :, 2:] = qs.view(np.uint8)
+    return out.reshape(rows, nb * 34)
+
+
+def q8_0_dequant(w: np.ndarray, ne0: int) -> np.ndarray:
+    """Q8_0 bytes [rows, ne0/32*34] -> f32 [rows, ne0] (d * qs)."""
+    rows = w.shape[0]
+    nb = ne0 // 32
+    b = np.ascontiguousarray(w).reshape(rows, nb, 34)
+    d = b[:, :, :2].copy().view(np.float16).astype(np.float32).reshape(rows, nb, 1)
+    qs = b[:, :, 2:].copy().view(np.int8).astype(np.float32)
+    return (d * qs).reshape(rows, ne0)
+
+
+def wkb_q8(w: np.ndarray, d_n: int, d_v: int, n_head: int, q_nope: np.ndarray, mutant: int = 0) -> np.ndarray:
+    """GGML_OP_M4_WKB with a Q8_0 W_kb (m4-wkb.cu:21-69): w bytes [H * d_v, d_n/32*34];
+    q_nope f32 [nt, H, d_n] -> out [nt, H, d_v]."""
+    q = np.ascontiguousarray(q_nope, dtype=np.float32)
+    nt = q.shape[0]
+    out = np.empty((nt, n_head, d_v), dtype=np.float32)
+    rc = lib().orc_wkb_q8(_ptr(np.ascontiguousarray(w)), d_n, d_v, n_head, _ptr(q), nt, d_n * 4, n_head * d_n * 4,
+                          _ptr(out), d_v * 4, n_head * d_v * 4, mutant)
+    assert rc == 0
+    return out
+
+
+def wvb_q8(w: np.ndarray, d_in: int, d_out: int, n_head: int, x: np.ndarray, mutant: int = 0) -> np.ndarray:
+    """GGML_OP_M4_PHASE phase 1 (m4-phase.cu:52-88): w bytes [H * d_out, d_in/32*34]; x f32
+    [nt, H, d_in] -> out [nt, H, d_out]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nt = x.shape[0]
+    out = np.empty((nt, n_head, d_out), dtype=np.float32)
+    rc = lib().orc_wvb_q8(_ptr(np.ascontiguousarray(w)), d_in, d_out, n_head, _ptr(x), nt, d_in * 4,
+                          n_head * d_in * 4, _ptr(out), d_out * 4, n_head * d_out * 4, mutant)
+    assert rc == 0
+    return out
+
+
+def rope_yarn_corr_dims(n_dims: int, n_ctx_orig: int, freq_base: float, beta_fast: float, beta_slow: float):
+    d = np.zeros(2, dtype=np.float32)
+    lib().orc_rope_yarn_corr_dims(n_dims, n_ctx_orig, freq_base, beta_fast, beta_slow, _ptr(d))
+    return float(d[0]), float(d[1])
+
+
+def kvwrite(cur: np.ndarray, w: np.ndarray, d_lat: int, n_rope: int, nw: np.ndarray, kcache_bits: np.ndarray,
+            kidx: int, pos: int, rp: dict, mutant: int = 0) -> np.ndarray:
+    """GGML_OP_M4_PHASE phase 0 (m4-phase.cu:95-200).  kcache_bits (uint16 [n_kv, >= d_lat + n_rope])
+    is written in place (row kidx); returns dst = Kcur (f32 [d_lat + n_rope])."""
+    cur = np.ascontiguousarray(cur, dtype=np.float32)
+    assert kcache_bits.dtype == np.uint16 and kcache_bits.flags["C_CONTIGUOUS"]
+    dst = np.empty(d_lat + n_rope, dtype=np.float32)
+    rc = lib().orc_kvwrite(_ptr(cur), cur.shape[0], _ptr(np.ascontiguousarray(w)), d_lat, n_rope,
+                           _ptr(np.ascontiguousarray(nw, dtype=np.float32)), _ptr(kcache_bits),
+                           kcache_bits.shape[1] * 2, kidx, pos, rp["freq_base"], rp["freq_scale"],
+                           rp["ext_factor"], rp["attn_factor"], rp["beta_fast"], rp["beta_slow"], rp["eps"],
+                           rp["n_ctx_orig"], _ptr(dst), mutant)
+    assert rc == 0
+    return dst

@@ -159,3 +159,63 @@ def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
     monkeypatch.setattr(ops, "LIB_PATH", tmp_path / "missing.so")
     with pytest.raises(RuntimeError, match="no CPU path"):
         A.ggml_m4_wkb(torch.zeros((32, 512, 128)), torch.zeros((1, 32, 128)))
+
+
+# ------------------------------------------------------------------ quantised ops (reference geometry)
+def q8(rows_shape, ne0):
+    return A.Q8_0(torch.zeros(*rows_shape, ne0 // 32 * 34, dtype=torch.uint8), ne0)
+
+
+def test_supports_wkb_q8():
+    w = q8((32, 256), 64)                                    # the reference's W_kb, Q8_0 [64, 256, 32]
+    q = torch.zeros((1, 32, 128))
+    assert A.supports_wkb(w, q[:, :, :64], torch.zeros((1, 32, 256)))
+    assert A.supports_wkb(q8((32, 512), 128), torch.zeros((2, 32, 192))[:, :, :128], torch.zeros((2, 32, 512)))
+    assert not A.supports_wkb(q8((32, 256), 96), torch.zeros((1, 32, 96)), torch.zeros((1, 32, 256)))   # d_n 96
+    v = ops.view(w)
+    v.nb[0] = 36                                             # not a packed Q8_0 row
+    assert A.load_library().mla_m4_supports_wkb(ctypes.byref(v), ctypes.byref(ops.view(q[:, :, :64])),
+                                                ctypes.byref(ops.view(torch.zeros((1, 32, 256))))) == 0
+
+
+def test_supports_phase_wvb():
+    w = q8((32, 128), 256)                                   # the reference's attn_v_b, Q8_0 [256, 128, 32]
+    assert A.supports_phase_wvb(w, torch.zeros((32, 1, 256)), torch.zeros((32, 1, 128)))
+    assert A.supports_phase_wvb(q8((32, 128), 512), torch.zeros((32, 7, 512)), torch.zeros((32, 7, 128)))
+    assert not A.supports_phase_wvb(w, torch.zeros((32, 1, 256)), torch.zeros((32, 2, 128)))      # nt mismatch
+    assert not A.supports_phase_wvb(q8((32, 128), 96), torch.zeros((32, 1, 96)), torch.zeros((32, 1, 128)))
+    assert not A.supports_phase_wvb(w, torch.zeros((32, 1, 256), dtype=torch.float16), torch.zeros((32, 1, 128)))
+
+
+def kv_descs(n_embd=4096, d_lat=256, n_dims=64, n_kv=100):
+    n_out = d_lat + n_dims
+    return (torch.zeros(n_embd), q8((n_out,), n_embd), torch.zeros(d_lat), torch.zeros((n_kv, n_out), dtype=torch.float16),
+            torch.zeros(1, dtype=torch.int64), torch.zeros(1, dtype=torch.int32))
+
+
+RP = dict(freq_base=10000.0, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, beta_fast=32.0, beta_slow=1.0, eps=1e-6,
+          n_ctx_orig=4096)
+
+
+def test_supports_phase_kvwrite():
+    rp = A.rope_params(n_dims=64, **RP)
+    assert A.supports_phase_kvwrite(*kv_descs(), rp, torch.zeros(320))                       # the reference's
+    assert A.supports_phase_kvwrite(*kv_descs(7168, 512), rp, torch.zeros(576))                # 576-wide cache
+    assert not A.supports_phase_kvwrite(*kv_descs(), rp, torch.zeros(321))                     # dst width
+    assert not A.supports_phase_kvwrite(*kv_descs(n_embd=2048), rp, torch.zeros(320))          # n_embd
+    d = list(kv_descs())
+    d[4] = torch.zeros(1, dtype=torch.int32)                                                   # kidx must be I64
+    assert not A.supports_phase_kvwrite(*d, rp, torch.zeros(320))
+    bad = A.rope_params(n_dims=64, **{**RP, "freq_base": 0.0})
+    assert not A.supports_phase_kvwrite(*kv_descs(), bad, torch.zeros(320))
+
+
+def test_phase_entry_points_reject_before_launching():
+    lib = A.load_library()
+    P = ctypes.byref
+    w, x, out = ops.view(q8((32, 128), 256)), ops.view(torch.zeros((32, 1, 256))), ops.view(torch.zeros((32, 1, 128)))
+    assert lib.mla_m4_phase_wvb(P(w), None, P(out), None) == -1
+    descs = [ops.view(t) for t in kv_descs()]
+    assert lib.mla_m4_phase_kvwrite(*(P(v) for v in descs), None, P(ops.view(torch.zeros(320))), None) == -1
+    assert lib.mla_m4_phase_kvwrite(*(P(v) for v in descs), P(A.rope_params(n_dims=64, **RP)),
+                                    P(ops.view(torch.zeros(300))), None) == -3
