@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time S in {64,128,192,256}")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm", action="store_true", help="also report WARM (one cache) timings")
+    ap.add_argument("--ops", action="store_true",
+                    help="time the reference-geometry quantised ops (Q8_0 WKB, PHASE wv_b, PHASE KV-write) instead")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="no timing: run the calibration copy and a few steps, for rocprofv3 --pmc")
     return ap.parse_args()
@@ -63,6 +65,8 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     A.load_library()
+    if args.ops:
+        return ops_bench(args)
     inp = I.make_config(args.config)
     if inp.nt > 1:
         return prefill_bench(args, inp)
@@ -322,6 +326,91 @@ def prefill_bench(args, inp) -> int:
                                              "frac": round(tf_attn / 2500.0, 4), "splits": n_split}},
            "cpu_baseline": None,
            "extra": {"us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2), "us_phase_merge": round(us_merge, 2)}}
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+def ops_bench(args) -> int:
+    """The reference geometry's quantised ops (the shapes its builders assert: ggml.c:3405-3539),
+    each COLD (weights rotated over more copies than the 256 MB MALL holds), graph-replayed, HIP
+    events.  Algorithmic bytes: weights + activations + outputs (+ the f16 cache row for KV-write).
+    Reference figures (RX 9070, m4-wkb.cu:11-12 and m4-phase.cu:8,31) are printed beside them."""
+    import torch
+    import aubier_amd as A
+    from aubier_amd import inputs as I
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(9100)
+
+    def q8_blocks(rows, ne0, copies):
+        nb = ne0 // 32
+        b = np.empty((rows, nb, 34), dtype=np.uint8)
+        b[:, :, :2] = (np.abs(rng.standard_normal((rows, nb))) * 0.01 + 0.001).astype(np.float16).view(np.uint8).reshape(rows, nb, 2)
+        b[:, :, 2:] = rng.integers(-127, 128, size=(rows, nb, 32)).astype(np.int8).view(np.uint8)
+        t = torch.from_numpy(b.reshape(rows, nb * 34)).to(dev)
+        return [t] + [t.clone() for _ in range(copies - 1)]
+
+    def timed(fn, n):
+        for i in range(2):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (reps * n)
+
+    res = {}
+    H = 32
+    # WKB, Q8_0 W_kb [64, 256, 32] (0.53 MiB), q_nope with the 128-float head stride
+    nrot = 600
+    ws = q8_blocks(H * 256, 64, nrot)
+    q = torch.from_numpy(rng.standard_normal((1, H, 128)).astype(np.float32) * 0.05).to(dev)
+    out = torch.empty((1, H, 256), dtype=torch.float32, device=dev)
+    us = timed(lambda i: A.ggml_m4_wkb(A.Q8_0(ws[i % nrot].view(H, 256, 68), 64), q[:, :, :64], out=out), nrot)
+    by = H * 256 * 68 + H * 64 * 4 + H * 256 * 4
+    res["wkb_q8_0"] = {"shape": "Q8_0 [64,256,32] x f32 [64,32,1] -> [256,32,1]", "us": round(us, 3), "bytes": by,
+                       "GBps": round(by / (us * 1e3), 1), "reference_rx9070_us": 4.05}
+    del ws
+    # PHASE 1 wv_b, Q8_0 [256, 128, 32] (1.06 MiB)
+    nrot = 300
+    ws = q8_blocks(H * 128, 256, nrot)
+    x = torch.from_numpy(rng.standard_normal((H, 1, 256)).astype(np.float32) * 0.05).to(dev)
+    out = torch.empty((H, 1, 128), dtype=torch.float32, device=dev)
+    us = timed(lambda i: A.ggml_m4_phase_wvb(A.Q8_0(ws[i % nrot].view(H, 128, 272), 256), x, out=out), nrot)
+    by = H * 128 * 272 + H * 256 * 4 + H * 128 * 4
+    res["phase1_wvb"] = {"shape": "Q8_0 [256,128,32] x f32 [256,1,32] -> [128,1,32]", "us": round(us, 3), "bytes": by,
+                         "GBps": round(by / (us * 1e3), 1), "reference_rx9070_stock_us": 16.6}
+    del ws
+    # PHASE 0 KV-write, Q8_0 [4096, 320] (1.36 MiB), a 32,768-row cache
+    nrot = 250
+    ws = q8_blocks(320, 4096, nrot)
+    cur = torch.from_numpy(rng.standard_normal(4096).astype(np.float32)).to(dev)
+    nw = torch.ones(256, dtype=torch.float32, device=dev)
+    kc = torch.zeros((32768, 320), dtype=torch.float16, device=dev)
+    kidx = torch.tensor([12345], dtype=torch.int64, device=dev)
+    pos = torch.tensor([12345], dtype=torch.int32, device=dev)
+    rp = A.rope_params(freq_base=1e6, freq_scale=0.25, ext_factor=1.0, attn_factor=1.0, beta_fast=32.0, beta_slow=1.0,
+                       eps=1e-6, n_dims=64, n_ctx_orig=8192)
+    out = torch.empty(320, dtype=torch.float32, device=dev)
+    us = timed(lambda i: A.ggml_m4_phase_kvwrite(cur, A.Q8_0(ws[i % nrot], 4096), nw, kc, kidx, pos, rp, out=out), nrot)
+    by = 320 * 128 * 34 + 4096 * 4 + 256 * 4 + 320 * 4 + 320 * 2
+    res["phase0_kvwrite"] = {"shape": "Q8_0 [4096,320] gemv + norm + YaRN rope + f16 scatter (2 launches)",
+                             "us": round(us, 3), "bytes": by, "GBps": round(by / (us * 1e3), 1),
+                             "reference_rx9070_stock_us": 29.4}
+    for v in res.values():
+        v["frac_of_hbm_peak"] = round(v["GBps"] / HBM_PEAK_GBPS, 4)
+    rec = {"metric": "reference-geometry quantised ops: us per launch (COLD) and achieved GB/s", "value": None,
+           "unit": "us", "n_gpus": 1, "dtype": "q8_0/f32", "data": "synthetic", "ops": res,
+           "note": "latency-bound launches of ~1 MB; the reference figures are per layer on an RX 9070"}
     print(json.dumps(rec), flush=True)
     return 0
 
