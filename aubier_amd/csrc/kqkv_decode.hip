@@ -42,19 +42,12 @@ struct ShortCfg {
     static constexpr int DVQ = DV / NWAVE;              // output columns per wave
     static constexpr int NTQ = DVQ / 32;                // 32-column output tiles per wave
     static constexpr int PROW = TK + 8;                 // P exchange row pitch (halves)
-    static constexpr int OREG = DVQ * HG * 2;           // a wave's f16 [DVQ][32 heads] output region
-    static constexpr int OPT = HG * DVQ / 8 / 64;       // 16-byte output chunks per lane
-    static_assert(OREG <= G::ROWS_BYTES, "a wave's output region fits its slot of a stage");
+    static constexpr int OPITCH = DVQ * 2 + 16;         // f16 output staging row pitch (bytes)
+    static constexpr int CPR = DVQ / 8;                 // 16-byte output chunks per head row
+    static_assert(HG * OPITCH <= G::ROWS_BYTES, "a wave's output staging fits its slot of a stage");
+    static_assert(CPR % 2 == 0, "whole rounds of 64 chunks");
     static_assert(NWAVE * NTQ - 1 < 64, "P.V operand offsets fit the DS immediate");
 };
-
-// Unit swizzle of the output regions ([DVQ rows][32 heads] f16, rows of 8 8-byte units): unit u of
-// row dv sits at slot u ^ ounit(dv), ounit = 4 b1 ^ b2 ^ 6 b3 ^ 2 b4 (b_i = bit i of dv).  The
-// stores (32 consecutive rows, one unit) and the transpose reads (4 rows x 4 units per 16 lanes,
-// rows 8 apart across 16-lane pairs) then hit distinct banks at 128 or 256 bytes per LDS clock.
-__device__ __forceinline__ int ounit(int dv) {
-    return (((dv >> 1) & 1) << 2) ^ ((dv >> 2) & 1) ^ (((dv >> 3) & 1) * 6) ^ (((dv >> 4) & 1) << 1);
-}
 
 template <int DK, int DV>
 __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) {
@@ -63,7 +56,6 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     __shared__ __attribute__((aligned(16))) char ring[G::RING];          // [stage][wave] K rows + mask
     __shared__ __attribute__((aligned(16))) half_t px[2][HG * C::PROW];  // P exchange, by tile parity
     __shared__ __attribute__((aligned(16))) float red[2][HG][NWAVE];     // slice maxima [head][wave], by tile parity
-    __shared__ __attribute__((aligned(16))) float inv_w[NWAVE][HG];      // 1 / l per head, one copy per wave
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -84,7 +76,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     // sum of the P values this lane feeds to the P.V MFMAs: head lane & 31, keys 8 (lane >> 5) .. +7
     // of each 16-key slice (the lane ^ 32 holds the other half)
     float l_acc = 0.0f;
-    f32x16 o[C::NTQ];                        // tile i: C row = head, C col = column DVQ w + 32 i + (lane & 31)
+    // o^T tile i: C row = column DVQ w + 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3), C col = head lane & 31
+    f32x16 o[C::NTQ];
 #pragma unroll
     for (int i = 0; i < C::NTQ; ++i)
 #pragma unroll
@@ -145,18 +138,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
             }
             l_acc *= al[(lane >> 4) & 1];         // this lane's head is 16 ((lane >> 4) & 1) + j16
             if (k > 0) {                          // (on the first tile the accumulators are still 0)
-                // accumulator rows are heads 8 (r / 4) + 4 (lane >> 5) + (r & 3): fetch their
-                // factors from the lanes holding them (head h's in lane h & 15 of set n = h >> 4)
-                f32x16 al16;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int h = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    const float a0 = __shfl(al[0], h & 15, 64), a1 = __shfl(al[1], h & 15, 64);
-                    al16[r] = (h >> 4) ? a1 : a0;
-                }
-                // In place on the accumulator registers, one asm block per element, so that they
-                // stay in AGPRs across this branch (a plain multiply makes the register allocator
-                // move the tile set through VGPRs).  The s_nops cover the MFMA -> VALU read distance.
+                // every accumulator column is this lane's head: one factor per lane.  In place on
+                // the accumulator registers, one asm block per element, so that they stay in AGPRs
+                // across this branch; the s_nops cover the MFMA -> VALU read distance.
+                const float a_own = al[(lane >> 4) & 1];
                 asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
                 for (int i = 0; i < C::NTQ; ++i)
@@ -164,7 +149,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
                     for (int r = 0; r < 16; ++r) {
                         float tmp;
                         asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
-                                     : "+a"(o[i][r]), "=&v"(tmp) : "v"(al16[r]));
+                                     : "+a"(o[i][r]), "=&v"(tmp) : "v"(a_own));
                     }
                 asm volatile("s_nop 7" ::: "memory");
             }
@@ -172,8 +157,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
             __syncthreads();
         }
 
-        // O[:, own columns] += P . V over the tile's 64 keys (4 slices x 16); the operands of
-        // slice ks + 1 are read while the MFMAs of slice ks run
+        // O^T[own columns, heads] += V^T . P^T over the tile's 64 keys (4 slices x 16): the V
+        // operand (column, 8 keys per lane) and the P rows (head, 8 keys per lane) are the A and B
+        // operands of the 32x32x16 MFMA.  The operands of slice ks + 1 are read while the MFMAs
+        // of slice ks run.
         {
             half8 pa[2], vb[2][C::NTQ];
             auto load = [&](int ks, int b) {
@@ -189,7 +176,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < C::NTQ; ++i)
-                    o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[ks & 1], vb[ks & 1][i], o[i], 0, 0, 0);
+                    o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb[ks & 1][i], pa[ks & 1], o[i], 0, 0, 0);
                 const half8 pp = pa[ks & 1];
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) l_acc = __builtin_amdgcn_fdot2(half2{pp[e], pp[e + 1]}, ONE2, l_acc, false);
@@ -210,23 +197,20 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     // workgroup barrier from here on.  The header is (m_ref, l): m_ref lies within 2^8 below the
     // split's max, which the merge's algebra does not care about (only m + ln l enters it).
     const float L = l_acc + shfl_xor(l_acc, 32);         // head lane_e & 31
-    float * invw = inv_w[w];
-    if (lane_e < HG) invw[lane_e] = L > 0.0f ? 1.0f / L : 0.0f;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const int hl = lane_e & 31, hi4 = 4 * (lane_e >> 5);
 
     const bool direct = a.dst != nullptr;                 // single split: final f32 output to dst
     if (direct) {
+        const int h = hg0 + hl;
+        if (h < a.n_head) {
+            float * d = a.dst + ((size_t)h * a.nt + t) * DV + C::DVQ * w + hi4;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const f32x4 s4 = *reinterpret_cast<const f32x4 *>(&invw[8 * q4 + 4 * (lane_e >> 5)]);
+            for (int i = 0; i < C::NTQ; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int h = hg0 + 8 * q4 + 4 * (lane_e >> 5) + e;
-                if (h < a.n_head) {
-                    float * d = a.dst + ((size_t)h * a.nt + t) * DV + C::DVQ * w + (lane_e & 31);
-#pragma unroll
-                    for (int i = 0; i < C::NTQ; ++i) d[32 * i] = o[i][4 * q4 + e] * s4[e];
-                }
-            }
+                for (int q4 = 0; q4 < 4; ++q4)
+                    *reinterpret_cast<f32x4 *>(d + 32 * i + 8 * q4) =
+                        f32x4{o[i][4 * q4] * inv, o[i][4 * q4 + 1] * inv, o[i][4 * q4 + 2] * inv, o[i][4 * q4 + 3] * inv};
         }
         return;
     }
@@ -236,41 +220,25 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         reinterpret_cast<float *>(blk)[lane_e] = (mr == -INFINITY) ? -INFINITY : mr * LN2;   // natural-log units
         reinterpret_cast<float *>(blk)[HG + lane_e] = L;
     }
-    // o / l in f16 into this wave's own slice of the stage the last tile did not use (no wave
+    // o / l in f16 through this wave's own slot of the stage the last tile did not use (no wave
     // reads it any more: the last tile's loop-top barrier follows every P.V of the one before),
-    // [DVQ rows][32 heads], then read back transposed into [32 heads][D_v] chunks of 8 columns.
-    // Write and read are the same wave's, in LDS order.
-    char * reg = ring + ss.stage_off(n_my & 1, w);
-    {
-        const int dvl = lane_e & 31, hi32 = lane_e >> 5;
+    // as [32 heads][DVQ] rows; then 16-byte chunks out, 4 head rows of 2 * DVQ bytes per
+    // instruction (whole cache lines).  Write and read are the same wave's, in LDS order.
+    char * stg = ring + ss.stage_off(n_my & 1, w);
+#pragma unroll
+    for (int i = 0; i < C::NTQ; ++i)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-            const f32x4 s4 = *reinterpret_cast<const f32x4 *>(&invw[8 * q4 + 4 * hi32]);
-#pragma unroll
-            for (int i = 0; i < C::NTQ; ++i) {
-                const int dv = 32 * i + dvl;
-                half4 hv;
-                hv[0] = to_half(o[i][4 * q4 + 0] * s4[0]);
-                hv[1] = to_half(o[i][4 * q4 + 1] * s4[1]);
-                hv[2] = to_half(o[i][4 * q4 + 2] * s4[2]);
-                hv[3] = to_half(o[i][4 * q4 + 3] * s4[3]);
-                *reinterpret_cast<half4 *>(reg + dv * 64 + 8 * ((2 * q4 + hi32) ^ ounit(dv))) = hv;
-            }
+            const half4 hv = {to_half(o[i][4 * q4] * inv), to_half(o[i][4 * q4 + 1] * inv), to_half(o[i][4 * q4 + 2] * inv),
+                              to_half(o[i][4 * q4 + 3] * inv)};
+            *reinterpret_cast<half4 *>(stg + hl * C::OPITCH + (32 * i + 8 * q4 + hi4) * 2) = hv;
         }
-    }
-    // per 64-chunk group cg: heads 16 hb + (lane & 15), columns 8 (4 (cg >> 1) + (lane >> 4)) .. +7
-    const int ge = lane_e >> 4, je = lane_e & 15;
 #pragma unroll
-    for (int cg = 0; cg < C::OPT; ++cg) {
-        const int hb = cg & 1;
-        const int dv8 = 4 * (cg >> 1) + ge;
-        const int dv_lo = 8 * dv8 + (je >> 2), dv_hi = dv_lo + 4;
-        const int u = 4 * hb + (je & 3);
-        const half4 lo = lds_read_tr16(reinterpret_cast<const half_t *>(reg + dv_lo * 64 + 8 * (u ^ ounit(dv_lo))));
-        const half4 hi = lds_read_tr16(reinterpret_cast<const half_t *>(reg + dv_hi * 64 + 8 * (u ^ ounit(dv_hi))));
-        const half8 hv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hv),
-                                    reinterpret_cast<u32x4 *>(blk + 256 + ((size_t)(16 * hb + je) * DV + C::DVQ * w + 8 * dv8) * 2));
+    for (int it = 0; it < C::CPR / 2; ++it) {
+        const int q = 64 * it + lane_e;
+        const int row = q / C::CPR, ch = q % C::CPR;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + row * C::OPITCH + 16 * ch);
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(blk + 256 + ((size_t)row * DV + C::DVQ * w + 8 * ch) * 2));
     }
 }
 
