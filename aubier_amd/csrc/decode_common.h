@@ -256,10 +256,7 @@ __device__ __forceinline__ void slice_scores(const DecodeArgs & a, const f32x4 &
         mx[1] = fmaxf(mx[1], sc[1][r]);
     }
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-        mx[n] = fmaxf(mx[n], shfl_xor(mx[n], 16));
-        mx[n] = fmaxf(mx[n], shfl_xor(mx[n], 32));
-    }
+    for (int n = 0; n < 2; ++n) mx[n] = rows4_max(mx[n]);
 }
 
 }  // namespace decode

@@ -196,7 +196,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     // Every wave summed the whole P exchange for its heads, so each finishes on its own: no
     // workgroup barrier from here on.  The header is (m_ref, l): m_ref lies within 2^8 below the
     // split's max, which the merge's algebra does not care about (only m + ln l enters it).
-    const float L = l_acc + shfl_xor(l_acc, 32);         // head lane_e & 31
+    const float L = halves_sum(l_acc);         // head lane_e & 31
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     const int hl = lane_e & 31, hi4 = 4 * (lane_e >> 5);
 

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
     const int hl = lane_e & 31;
 
     // ---- merge of the four waves' states, per head ----
-    const float lw = l_acc + shfl_xor(l_acc, 32);         // head hl, all of this wave's keys
+    const float lw = halves_sum(l_acc);         // head hl, all of this wave's keys
     if (lane_e < HG) {
         fin_m[lane_e][w] = m_run[(lane_e >> 4) & 1];      // lane_e's head is 16 ((lane_e >> 4) & 1) + j16
         fin_l[lane_e][w] = lw;

@@ -191,7 +191,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
     asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"(tid));
     const int lane_e = tid_e & 63;
     const int hl = lane_e & 31;
-    const float L = l_acc + shfl_xor(l_acc, 32);         // head hl, all keys of the split
+    const float L = halves_sum(l_acc);         // head hl, all keys of the split
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     if (!token_live) return;
     const int hi4 = 4 * (lane_e >> 5);

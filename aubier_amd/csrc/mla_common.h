@@ -28,6 +28,22 @@ __device__ __forceinline__ half_t to_half(float x) { return (half_t)x; }
 // Cross-lane shuffles over the full 64-lane wavefront.
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, WAVE); }
 
+// Max / sum over the four 16-lane rows of a wavefront (lanes j, j + 16, j + 32, j + 48) with the
+// gfx950 row-swap instructions: v_permlane16_swap(x, x) leaves (row 0 | row 0 | row 2 | row 2) and
+// (row 1 | row 1 | row 3 | row 3), v_permlane32_swap(x, x) (low half | low half) and (high | high):
+// two VALU ops per step instead of an LDS permute round trip.
+__device__ __forceinline__ float rows4_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+// the value of lane l ^ 32 added to lane l's (the two 32-lane halves summed)
+__device__ __forceinline__ float halves_sum(float v) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
