@@ -28,7 +28,7 @@ template <int DK>
 struct SliceGeom {
     static_assert(DK % 64 == 0, "geometry");
     static constexpr int CH = DK * 2 / 16;              // 16-byte chunks per cache row
-    static_assert(CH % 4 == 0, "1 KB slot blocks of 4 chunks x 16 rows");
+    static_assert(CH % 8 == 0, "1 KB slot blocks of 8 rows x 8 chunks");
     static constexpr int DMA_N = WK * CH / 64;          // 16-byte DMA instructions per slice
     static constexpr int ROWS_BYTES = WK * DK * 2;
     static constexpr int STAGE = ROWS_BYTES + 256;      // 16 K rows + the mask slot
@@ -41,30 +41,37 @@ struct SliceGeom {
     static_assert(QSTEPS == DMA_N, "one DMA block per Q.K^T step");
 };
 
-// Slot layout (one wave slice, 16 cache rows): 1 KB blocks i = 0 .. CH/4 - 1, block i holding chunks
-// 4 i .. 4 i + 3 (16 bytes each) of the 16 rows, chunk 4 i + q of row r at slot 16 q + (r ^ 4 q).
-// DMA instruction i fills block i, lane l fetching row (l & 15) ^ 4 (l >> 4), chunk 4 i + (l >> 4),
-// so its global offset is lane-only plus 64 i.  The XOR keeps the Q.K^T reads (16 rows, one chunk)
-// and the transpose reads (4 rows x 4 chunks per 32 lanes) on distinct banks, at 128 or 256 bytes
-// per LDS clock alike.
-__device__ __forceinline__ int slot_of(int r, int q) { return 16 * q + (r ^ (4 * q)); }
+// Slot layout (one wave slice, 16 cache rows of CH 16-byte chunks): 1 KB blocks b = 0 .. CH/4 - 1,
+// block b holding rows 8 (b & 1) .. +7 and chunks 8 (b >> 1) .. +7 -- one 128-byte segment of each
+// of 8 rows.  Row r, chunk c of the block sits at slot 16 ((r & 7) >> 1) + 8 (r & 1) + (c ^ row_sw(r)).
+// DMA instruction b fills block b (lane l -> slot l), so quarter-wave qq fetches rows 2 qq, 2 qq + 1
+// as two whole 128-byte segments: whole cache lines per request (a layout that splits each line over
+// two instructions streams ~20% slower per CU).  The swizzle keeps on distinct banks, at 128 and 256
+// bytes per LDS clock alike, both the Q.K^T reads (16 rows, one chunk) and the transpose reads of
+// P.V (4 rows x 2 chunks per 16 lanes, 4 rows x 4 chunks per 32 lanes).  Chunk c + 4 of a row
+// (c & 4 == 0) is at the byte offset of chunk c XOR 64, chunk c + 8 at + 2048.
+__device__ __forceinline__ int row_sw(int r) { return ((2 * (r & 3)) | ((r >> 2) & 1)) ^ (2 * ((r >> 3) & 1)); }
+__device__ __forceinline__ int slot_byte(int r, int c) {
+    return 1024 * (2 * (c >> 3) + (r >> 3)) + 256 * ((r & 7) >> 1) + 128 * (r & 1) + 16 * ((c & 7) ^ row_sw(r));
+}
 
 // Where the V^T / V operand of P.V comes from: two transpose reads per 32-column tile, in 16-lane
 // group g lane j supplying row 8 (g >> 1) + (j >> 2) (then + 4) of a slice, 4 columns at
 // 32 i + 16 (g & 1) + 4 (j & 3).  Lane l then holds column 32 i + (l & 31), keys 8 (l >> 5) .. +7.
 struct PvAddr {
-    int lo, hi;
+    int lo, hi;                              // tile 0 (chunks 0 .. 3)
     __device__ __forceinline__ explicit PvAddr(int lane) {
         const int g = lane >> 4, j16 = lane & 15;
         const int r0 = 8 * (g >> 1) + (j16 >> 2);
         const int cq = 2 * (g & 1) + ((j16 & 3) >> 1);
-        lo = 16 * slot_of(r0, cq) + 8 * (j16 & 1);
-        hi = 16 * slot_of(r0 + 4, cq) + 8 * (j16 & 1);
+        lo = slot_byte(r0, cq) + 8 * (j16 & 1);
+        hi = slot_byte(r0 + 4, cq) + 8 * (j16 & 1);
     }
-    // the operand of 32-column tile i of the slice at sb
+    // the operand of 32-column tile i (chunks 4 i .. 4 i + 3) of the slice at sb
     __device__ __forceinline__ half8 load(const char * sb, int i) const {
-        const half4 l4 = lds_read_tr16(reinterpret_cast<const half_t *>(sb + lo + 1024 * i));
-        const half4 h4 = lds_read_tr16(reinterpret_cast<const half_t *>(sb + hi + 1024 * i));
+        const int x = 64 * (i & 1), o = 2048 * (i >> 1);
+        const half4 l4 = lds_read_tr16(reinterpret_cast<const half_t *>(sb + (lo ^ x) + o));
+        const half4 h4 = lds_read_tr16(reinterpret_cast<const half_t *>(sb + (hi ^ x) + o));
         return half8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
     }
 };
@@ -80,7 +87,7 @@ struct SliceStream {
     const float * mrow;     // this token's mask row (or any valid pointer when there is none)
     bool has_mask;
     int n_kv, n_tiles, t0, n_my, w;
-    uint32_t ring_lds, kvoff, mvoff;
+    uint32_t ring_lds, kvoff0, kvoff1, mvoff;  // lane offsets of even / odd row blocks, of the mask
 
     __device__ __forceinline__ SliceStream(const DecodeArgs & a, int sp, int t, int w_, uint32_t ring_lds_, int lane) {
         kc = a.kc;
@@ -96,7 +103,10 @@ struct SliceStream {
         n_my = base_t + (sp < rem ? 1 : 0);
         w = w_;
         ring_lds = ring_lds_;
-        kvoff = (uint32_t)(((lane & 15) ^ (4 * (lane >> 4))) * kc_nb1) + 16u * (uint32_t)(lane >> 4);
+        // lane l = 16 qq + 8 h + x of block b: row 8 (b & 1) + 2 qq + h, chunk 8 (b >> 1) + (x ^ row_sw(row))
+        const int r0 = 2 * (lane >> 4) + ((lane >> 3) & 1);
+        kvoff0 = (uint32_t)(r0 * kc_nb1) + 16u * (uint32_t)((lane & 7) ^ row_sw(r0));
+        kvoff1 = (uint32_t)((r0 + 8) * kc_nb1) + 16u * (uint32_t)((lane & 7) ^ row_sw(r0 + 8));
         mvoff = 4u * (uint32_t)(lane & 15);
     }
     __device__ __forceinline__ int stage_off(int s, int v) const { return (s * NWAVE + v) * G::STAGE; }
@@ -113,10 +123,17 @@ struct SliceStream {
         d.sb = ring_lds + (uint32_t)stage_off(s, w);
         return d;
     }
-    // instruction i < DMA_N: block i of the rows; i == DMA_N: the mask slot (float l = key key0 + (l & 15))
+    // instruction i < DMA_N: block i of the rows (NT: streaming cache policy); i == DMA_N: the mask
+    // slot (float l = key key0 + (l & 15))
+    template <bool NT = true>
     __device__ __forceinline__ void put(const SliceDma & d, int i) const {
-        if (i < G::DMA_N) dma16_nt(d.krs, kvoff, (uint32_t)(64 * i), d.sb + (uint32_t)(1024 * i));
-        else dma4(d.mrs, mvoff, 0u, d.sb + (uint32_t)G::ROWS_BYTES);
+        if (i < G::DMA_N) {
+            const uint32_t vo = (i & 1) ? kvoff1 : kvoff0, so = 128u * (uint32_t)(i >> 1);
+            if constexpr (NT) dma16_nt(d.krs, vo, so, d.sb + (uint32_t)(1024 * i));
+            else dma16(d.krs, vo, so, d.sb + (uint32_t)(1024 * i));
+        } else {
+            dma4(d.mrs, mvoff, 0u, d.sb + (uint32_t)G::ROWS_BYTES);
+        }
     }
 };
 
@@ -183,8 +200,9 @@ __device__ __forceinline__ void stage_q(const DecodeArgs & a, const SliceStream<
 
 // S^T = K . Q^T for the wave's 16 keys of the slice at sb (C rows = keys 4 g + r, C cols = heads
 // j16 (acc0) and 16 + j16 (acc1)).  DMA accounting (instructions complete in issue order): the
-// slice is DMA_N blocks then the mask; before the read of block b, the blocks after it, the mask
-// and the next slice's instructions issued so far (one per completed step) may still be in flight.
+// slice is DMA_N blocks then the mask, step s reading blocks 2 (s >> 1) and 2 (s >> 1) + 1; before
+// that read, the blocks after them, the mask and the next slice's instructions issued so far (one
+// per completed step) may still be in flight.
 // With DMA, the next slice's DMA (dn) is spread over the steps.  Operand reads run QPF steps ahead
 // of their MFMAs; the scheduling barriers keep the compiler from sinking them back next to their
 // use.  Two accumulator chains per head tile (even / odd steps) keep consecutive MFMAs
@@ -199,18 +217,23 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
     const int g = lane >> 4, j16 = lane & 15;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     f32x4 acc2 = {0.f, 0.f, 0.f, 0.f}, acc3 = {0.f, 0.f, 0.f, 0.f};
-    const char * abase = sb + 16 * slot_of(j16, g);     // row j16, chunk 4 s + g of block s
+    static_assert(QPF % 2 == 0, "operand reads ahead by whole block pairs");
+    // row j16, chunk 4 s + g: step s at (a0 ^ 64 (s & 1)) + 2048 (s >> 1)
+    const int a0 = slot_byte(j16, g);
+    auto arow = [&](int st) { return reinterpret_cast<const half8 *>(sb + (a0 ^ (64 * (st & 1))) + 2048 * (st >> 1)); };
     half8 abuf[QPF];
-    if constexpr (WAIT) wait_vm<G::DMA_N + 1 - QPF>();
+    if constexpr (WAIT) wait_vm<G::DMA_N + 1 - QPF>();      // blocks 0 .. QPF - 1
 #pragma unroll
-    for (int s = 0; s < QPF; ++s) abuf[s] = *reinterpret_cast<const half8 *>(abase + 1024 * s);
+    for (int s = 0; s < QPF; ++s) abuf[s] = *arow(s);
 #pragma unroll
     for (int s = 0; s < G::QSTEPS; ++s) {
         const half8 av = abuf[s % QPF];
         if (s + QPF < G::QSTEPS) {
-            if constexpr (DMA) wait_vm<G::DMA_N - QPF>();
-            else if constexpr (WAIT) wait_vm_le(G::DMA_N - QPF - s);
-            abuf[s % QPF] = *reinterpret_cast<const half8 *>(abase + 1024 * (s + QPF));
+            // blocks 0 .. 2 ((s + QPF) >> 1) + 1 landed; s instructions of the next slice issued
+            const int later = G::DMA_N - 1 - 2 * ((s + QPF) >> 1);
+            if constexpr (DMA) wait_vm_le(later + s);
+            else if constexpr (WAIT) wait_vm_le(later);
+            abuf[s % QPF] = *arow(s + QPF);
         }
         if (s & 1) {
             acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc2, 0, 0, 0);

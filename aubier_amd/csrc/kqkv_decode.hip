@@ -88,7 +88,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
 
     for (int k = 0; k < n_my; ++k) {
         // every wave is past P.V of tile k - 1, so stage (k + 1) & 1 can take tile k + 1: its DMA
-        // is spread over this tile's Q.K^T steps, which the memory stream then paces
+        // is spread over this tile's Q.K^T steps, which the memory stream then paces (measured
+        // slightly faster than issuing tile 1 whole right after the q staging)
         if (k >= 1) __syncthreads();
         const SliceDma dn = ss.plan((k + 1) & 1, k + 1);
         const int par = k & 1;

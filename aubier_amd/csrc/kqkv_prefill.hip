@@ -66,7 +66,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
         const int mleft = a.n_kv - tile * TK;
         const i32x4 mrs = make_rsrc(ss.mrow + tile * TK, (ss.has_mask && mleft > 0) ? (uint32_t)mleft * 4u : 0u);
 #pragma unroll
-        for (int i = 0; i < G::DMA_N; ++i) dma16(d.krs, ss.kvoff, (uint32_t)(64 * i), d.sb + (uint32_t)(1024 * i));
+        for (int i = 0; i < G::DMA_N; ++i) ss.template put<false>(d, i);
         dma4(mrs, 4u * (uint32_t)lane, 0u, d.sb + (uint32_t)G::ROWS_BYTES);
     };
     issue(0, 0);
