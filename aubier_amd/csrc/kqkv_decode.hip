@@ -109,7 +109,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
                 half4 ph;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    ph[r] = to_half((sc[n][r] == -INFINITY) ? 0.0f : exp2_fast(fminf(sc[n][r] - m_ref[n], 15.0f)));
+                    ph[r] = to_half(exp2_unless(sc[n][r] == -INFINITY, fminf(sc[n][r] - m_ref[n], 15.0f)));
                 *reinterpret_cast<half4 *>(&pxv[(16 * n + j16) * C::PROW + WK * w + 4 * g]) = ph;
             }
         };

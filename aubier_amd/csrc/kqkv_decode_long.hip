@@ -118,10 +118,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
         uint32_t px[2], py[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const float x0 = (sc[0][2 * e] == -INFINITY) ? 0.0f : exp2_fast(sc[0][2 * e] - m_run[0]);
-            const float x1 = (sc[0][2 * e + 1] == -INFINITY) ? 0.0f : exp2_fast(sc[0][2 * e + 1] - m_run[0]);
-            const float y0 = (sc[1][2 * e] == -INFINITY) ? 0.0f : exp2_fast(sc[1][2 * e] - m_run[1]);
-            const float y1 = (sc[1][2 * e + 1] == -INFINITY) ? 0.0f : exp2_fast(sc[1][2 * e + 1] - m_run[1]);
+            const float x0 = exp2_unless(sc[0][2 * e] == -INFINITY, sc[0][2 * e] - m_run[0]);
+            const float x1 = exp2_unless(sc[0][2 * e + 1] == -INFINITY, sc[0][2 * e + 1] - m_run[0]);
+            const float y0 = exp2_unless(sc[1][2 * e] == -INFINITY, sc[1][2 * e] - m_run[1]);
+            const float y1 = exp2_unless(sc[1][2 * e + 1] == -INFINITY, sc[1][2 * e + 1] - m_run[1]);
             px[e] = __builtin_bit_cast(uint32_t, half2{to_half(x0), to_half(x1)});
             py[e] = __builtin_bit_cast(uint32_t, half2{to_half(y0), to_half(y1)});
             const auto sw = __builtin_amdgcn_permlane16_swap(px[e], py[e], false, false);
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
     const float M = fmaxf(fmaxf(mm[0], mm[1]), fmaxf(mm[2], mm[3]));
     float L = 0.0f;
 #pragma unroll
-    for (int v = 0; v < NWAVE; ++v) L += (mm[v] == -INFINITY) ? 0.0f : ll[v] * exp2_fast(mm[v] - M);
+    for (int v = 0; v < NWAVE; ++v) L += ll[v] * exp2_unless(mm[v] == -INFINITY, mm[v] - M);
     const float m_w = (w == 0) ? mm[0] : (w == 1) ? mm[1] : (w == 2) ? mm[2] : mm[3];
     const float cw = (m_w == -INFINITY || !(L > 0.0f)) ? 0.0f : exp2_fast(m_w - M) / L;   // this wave's weight
 

@@ -70,12 +70,12 @@ __global__ __launch_bounds__(256) void kqkv_generic_kernel(DecodeArgs a, int dk,
             const float s = sc[lane];
             const float tmax = wave_max(s);
             const float m_new = fmaxf(m_run, tmax);
-            const float p = (s == -INFINITY) ? 0.0f : exp2_fast(s - m_new);
+            const float p = exp2_unless(s == -INFINITY, s - m_new);
             ps[lane] = F16 ? (float)to_half(p) : p;
             const float tsum = wave_sum(p);
             if (lane == 0) {
                 st[0] = m_new;
-                st[1] = (m_run == -INFINITY) ? 0.0f : exp2_fast(m_run - m_new);
+                st[1] = exp2_unless(m_run == -INFINITY, m_run - m_new);
                 st[2] = tsum;
             }
         }
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void merge_few_kernel(const char * __restrict_
     float L = 0.0f;
     float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < n_split; ++s) {
-        const float f = (ms[s] == -INFINITY) ? 0.0f : ls[s] * exp2_fast((ms[s] - m) * LOG2E);
+        const float f = ls[s] * exp2_unless(ms[s] == -INFINITY, (ms[s] - m) * LOG2E);
         L += f;
         const OT * src = reinterpret_cast<const OT *>(base + (size_t)s * bb + 256) + (size_t)hh * dv + 8 * c8;
         if constexpr (sizeof(OT) == 2) {

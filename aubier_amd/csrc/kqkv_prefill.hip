@@ -156,10 +156,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
             uint32_t px[2], py[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const float x0 = (sc[0][2 * e] == -INFINITY) ? 0.0f : exp2_fast(sc[0][2 * e] - m_run[0]);
-                const float x1 = (sc[0][2 * e + 1] == -INFINITY) ? 0.0f : exp2_fast(sc[0][2 * e + 1] - m_run[0]);
-                const float y0 = (sc[1][2 * e] == -INFINITY) ? 0.0f : exp2_fast(sc[1][2 * e] - m_run[1]);
-                const float y1 = (sc[1][2 * e + 1] == -INFINITY) ? 0.0f : exp2_fast(sc[1][2 * e + 1] - m_run[1]);
+                const float x0 = exp2_unless(sc[0][2 * e] == -INFINITY, sc[0][2 * e] - m_run[0]);
+                const float x1 = exp2_unless(sc[0][2 * e + 1] == -INFINITY, sc[0][2 * e + 1] - m_run[0]);
+                const float y0 = exp2_unless(sc[1][2 * e] == -INFINITY, sc[1][2 * e] - m_run[1]);
+                const float y1 = exp2_unless(sc[1][2 * e + 1] == -INFINITY, sc[1][2 * e + 1] - m_run[1]);
                 px[e] = __builtin_bit_cast(uint32_t, half2{to_half(x0), to_half(x1)});
                 py[e] = __builtin_bit_cast(uint32_t, half2{to_half(y0), to_half(y1)});
                 const auto sw = __builtin_amdgcn_permlane16_swap(px[e], py[e], false, false);

@@ -20,6 +20,12 @@ constexpr float LN2 = 0.6931471805599453f;
 
 // v_exp_f32: 2^x (the kernels keep scores in log2 units)
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+// exp2_fast(x), or 0 where zero holds (a masked key, an empty accumulator), without a branch: the
+// exponential is taken unconditionally (x may then be NaN) and the result selected
+__device__ __forceinline__ float exp2_unless(bool zero, float x) {
+    const float e = exp2_fast(x);
+    return zero ? 0.0f : e;
+}
 
 // f32 -> f16 round-to-nearest-even (v_cvt_f16_f32 under the default round mode), the
 // conversion ggml-cpu's mul_mat applies to src1 when src0 is F16.

@@ -65,13 +65,13 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
         float mx = m;
 #pragma unroll
         for (int j = 0; j < J; ++j) mx = fmaxf(mx, ms[j]);
-        const float f0 = (m == -INFINITY) ? 0.0f : exp2_fast((m - mx) * LOG2E);
+        const float f0 = exp2_unless(m == -INFINITY, (m - mx) * LOG2E);
         L *= f0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) O[k] *= f0;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const float f = (ms[j] == -INFINITY) ? 0.0f : ls[j] * exp2_fast((ms[j] - mx) * LOG2E);
+            const float f = ls[j] * exp2_unless(ms[j] == -INFINITY, (ms[j] - mx) * LOG2E);
             L += f;
 #pragma unroll
             for (int k = 0; k < 8; ++k) O[k] += f * os[j][k];
@@ -84,8 +84,8 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
         const float m2 = shfl_xor(m, off);
         const float L2 = shfl_xor(L, off);
         const float M = fmaxf(m, m2);
-        const float f1 = (m == -INFINITY) ? 0.0f : exp2_fast((m - M) * LOG2E);
-        const float f2 = (m2 == -INFINITY) ? 0.0f : exp2_fast((m2 - M) * LOG2E);
+        const float f1 = exp2_unless(m == -INFINITY, (m - M) * LOG2E);
+        const float f2 = exp2_unless(m2 == -INFINITY, (m2 - M) * LOG2E);
         L = L * f1 + L2 * f2;
 #pragma unroll
         for (int k = 0; k < 8; ++k) O[k] = O[k] * f1 + shfl_xor(O[k], off) * f2;
@@ -107,7 +107,7 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
             float LL = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float f = (sm[i][c8] == -INFINITY) ? 0.0f : exp2_fast((sm[i][c8] - M) * LOG2E);
+                const float f = exp2_unless(sm[i][c8] == -INFINITY, (sm[i][c8] - M) * LOG2E);
                 LL += sL[i][c8] * f;
                 r0 += sO[i][c8][0] * f;
                 r1 += sO[i][c8][1] * f;
