@@ -215,11 +215,12 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         }
         return;
     }
-    char * blk = a.part + (((size_t)blockIdx.y * a.nt + t) * a.n_split + sp) * part_block_bytes(DV, 2);
+    char * rec = part_record(a.part, blockIdx.y, a.nt, t, a.n_split, DV, 2);
+    char * blk = rec + part_o_off(a.n_split, sp, DV, 2);
     if (w == 0 && lane_e < HG) {
         const float mr = m_ref[(lane_e >> 4) & 1];        // lane_e's head 16 ((lane_e >> 4) & 1) + j16
-        reinterpret_cast<float *>(blk)[lane_e] = (mr == -INFINITY) ? -INFINITY : mr * LN2;   // natural-log units
-        reinterpret_cast<float *>(blk)[HG + lane_e] = L;
+        *reinterpret_cast<f32x2 *>(rec + part_ml_off(a.n_split, lane_e, sp)) =
+            f32x2{(mr == -INFINITY) ? -INFINITY : mr * LN2, L};                   // m in natural-log units
     }
     // o / l in f16 through this wave's own slot of the stage the last tile did not use (no wave
     // reads it any more: the last tile's loop-top barrier follows every P.V of the one before),
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
         const int q = 64 * it + lane_e;
         const int row = q / C::CPR, ch = q % C::CPR;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + row * C::OPITCH + 16 * ch);
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(blk + 256 + ((size_t)row * DV + C::DVQ * w + 8 * ch) * 2));
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(blk + ((size_t)row * DV + C::DVQ * w + 8 * ch) * 2));
     }
 }
 

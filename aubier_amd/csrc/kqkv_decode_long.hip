@@ -228,11 +228,11 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
         }
         return;
     }
-    char * blk = a.part + (((size_t)blockIdx.y * a.nt + t) * a.n_split + sp) * part_block_bytes(DV, 2);
-    if (w == 0 && lane_e < HG) {
-        reinterpret_cast<float *>(blk)[lane_e] = (M == -INFINITY) ? -INFINITY : M * LN2;   // natural-log units
-        reinterpret_cast<float *>(blk)[HG + lane_e] = L;
-    }
+    char * rec = part_record(a.part, blockIdx.y, a.nt, t, a.n_split, DV, 2);
+    char * blk = rec + part_o_off(a.n_split, sp, DV, 2);
+    if (w == 0 && lane_e < HG)
+        *reinterpret_cast<f32x2 *>(rec + part_ml_off(a.n_split, lane_e, sp)) =
+            f32x2{(M == -INFINITY) ? -INFINITY : M * LN2, L};                     // m in natural-log units
     // f16 [32 heads][DVQ] staging in this wave's own (consumed) exchange area, then 16-byte rows
     // out: the same wave writes and reads it, in LDS order
     char * stg = xch(w, 0);
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
         const int q = 64 * it + lane_e;
         const int row = q / C::CPR, ch = q % C::CPR;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + row * C::OPITCH + 16 * ch);
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(blk + 256 + ((size_t)row * DV + C::DVQ * w + 8 * ch) * 2));
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(blk + ((size_t)row * DV + C::DVQ * w + 8 * ch) * 2));
     }
 }
 

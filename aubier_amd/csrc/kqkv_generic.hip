@@ -109,20 +109,19 @@ __global__ __launch_bounds__(256) void kqkv_generic_kernel(DecodeArgs a, int dk,
         }
         return;
     }
-    char * blk = a.part + (((size_t)(h / PART_HEADS) * a.nt + t) * a.n_split + sp) * part_block_bytes(dv, F16 ? 2 : 4);
+    constexpr int OB = F16 ? 2 : 4;
+    char * rec = part_record(a.part, h / PART_HEADS, a.nt, t, a.n_split, dv, OB);
     const int hh = h % PART_HEADS;
-    if (tid == 0) {
-        float * hdr = reinterpret_cast<float *>(blk);
-        hdr[hh] = (m_run == -INFINITY) ? -INFINITY : m_run * LN2;
-        hdr[PART_HEADS + hh] = l_run;
-    }
+    char * blk = rec + part_o_off(a.n_split, sp, dv, OB);
+    if (tid == 0)
+        *reinterpret_cast<f32x2 *>(rec + part_ml_off(a.n_split, hh, sp)) = f32x2{(m_run == -INFINITY) ? -INFINITY : m_run * LN2, l_run};
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
 #pragma unroll
     for (int i = 0; i < GMAX_OPT; ++i) {
         const int c = tid + 256 * i;
         if (c >= dv) continue;
-        if (F16) reinterpret_cast<half_t *>(blk + 256)[(size_t)hh * dv + c] = to_half(o[i] * inv);
-        else reinterpret_cast<float *>(blk + 256)[(size_t)hh * dv + c] = o[i] * inv;
+        if (F16) reinterpret_cast<half_t *>(blk)[(size_t)hh * dv + c] = to_half(o[i] * inv);
+        else reinterpret_cast<float *>(blk)[(size_t)hh * dv + c] = o[i] * inv;
     }
 }
 
@@ -163,13 +162,13 @@ __global__ __launch_bounds__(256) void merge_few_kernel(const char * __restrict_
     const int h = (int)((idx / c8n) % n_head);
     const int t = (int)(idx / ((int64_t)c8n * n_head));
     const int hh = h % PART_HEADS;
-    const size_t bb = part_block_bytes(dv, (int)sizeof(OT));
-    const char * base = part + ((size_t)(h / PART_HEADS) * nt + t) * n_split * bb;
+    const char * rec = part_record(part, h / PART_HEADS, nt, t, n_split, dv, (int)sizeof(OT));
     float ms[MERGE_FEW], ls[MERGE_FEW];
     float m = -INFINITY;
     for (int s = 0; s < n_split; ++s) {
-        ms[s] = reinterpret_cast<const float *>(base + (size_t)s * bb)[hh];
-        ls[s] = reinterpret_cast<const float *>(base + (size_t)s * bb)[PART_HEADS + hh];
+        const f32x2 ml = *reinterpret_cast<const f32x2 *>(rec + part_ml_off(n_split, hh, s));
+        ms[s] = ml[0];
+        ls[s] = ml[1];
         m = fmaxf(m, ms[s]);
     }
     float L = 0.0f;
@@ -177,7 +176,7 @@ __global__ __launch_bounds__(256) void merge_few_kernel(const char * __restrict_
     for (int s = 0; s < n_split; ++s) {
         const float f = ls[s] * exp2_unless(ms[s] == -INFINITY, (ms[s] - m) * LOG2E);
         L += f;
-        const OT * src = reinterpret_cast<const OT *>(base + (size_t)s * bb + 256) + (size_t)hh * dv + 8 * c8;
+        const OT * src = reinterpret_cast<const OT *>(rec + part_o_off(n_split, s, dv, (int)sizeof(OT))) + (size_t)hh * dv + 8 * c8;
         if constexpr (sizeof(OT) == 2) {
             const half8 v = *reinterpret_cast<const half8 *>(src);
 #pragma unroll

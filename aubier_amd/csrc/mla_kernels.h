@@ -7,17 +7,32 @@
 
 namespace mla {
 
-// Split-K partial block of one (32-head group, token, split), blocks ordered [group][token][split]:
-//   float m[32]        a reference for the split's scores, natural-log units: the exact max
-//                      (VALU kernel) or a running reference at most 8 ln 2 below it (MFMA decode
-//                      kernel); -inf if the split is empty.  The merge only uses m + ln l.
-//   float l[32]        sum_j exp(s_j - m)
-//   T     o[32][D_v]   o / l: the split's normalised softmax output, 0 for an empty split.  T is
-//                      the cache's element type: f16 for an f16 cache (|o / l| <= max|V|, so it
-//                      cannot overflow), f32 for an f32 cache.
+// Split-K partials of one (32-head group g, token t) form a record of n_split * part_block_bytes
+// bytes at part + (g * nt + t) * n_split * part_block_bytes, records ordered [group][token]:
+//   float2 ml[32][n_split]       (m, l) of head hh, split s at [hh][s]: one head's pairs are
+//                                contiguous, so the merge reads them as a few whole lines
+//   T      o[n_split][32][D_v]   split s's o / l
+// with
+//   m      a reference for the split's scores, natural-log units: the exact max (VALU kernel) or a
+//          running reference at most 8 ln 2 below it (MFMA kernels); -inf if the split is empty.
+//          The merge only uses m + ln l.
+//   l      sum_j exp(s_j - m)
+//   o / l  the split's normalised softmax output, 0 for an empty split.  T is the cache's element
+//          type: f16 for an f16 cache (|o / l| <= max|V|, so it cannot overflow), f32 for f32.
 constexpr int PART_HEADS = 32;
 __host__ __device__ constexpr size_t part_block_bytes(int dv, int o_bytes) {
     return 256 + (size_t)PART_HEADS * (size_t)o_bytes * (size_t)dv;
+}
+__host__ __device__ inline char * part_record(char * part, int g, int nt, int t, int n_split, int dv, int o_bytes) {
+    return part + ((size_t)g * nt + t) * (size_t)n_split * part_block_bytes(dv, o_bytes);
+}
+__host__ __device__ inline const char * part_record(const char * part, int g, int nt, int t, int n_split, int dv, int o_bytes) {
+    return part + ((size_t)g * nt + t) * (size_t)n_split * part_block_bytes(dv, o_bytes);
+}
+// byte offsets within a record: the (m, l) pair of (head hh, split s); split s's o block
+__host__ __device__ constexpr size_t part_ml_off(int n_split, int hh, int s) { return ((size_t)hh * n_split + s) * 8; }
+__host__ __device__ constexpr size_t part_o_off(int n_split, int s, int dv, int o_bytes) {
+    return (size_t)n_split * 256 + (size_t)s * PART_HEADS * (size_t)dv * (size_t)o_bytes;
 }
 
 // Split-K decode / generic attention launch arguments (byte strides throughout).

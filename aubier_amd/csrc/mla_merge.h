@@ -1,6 +1,5 @@
-// mla_merge.h -- the split-K merge of one unit (64 output columns of one head of one token),
-// shared by the PHASE merge kernel and the decode kernel's fused merge (mla_kernels.h describes
-// the partial blocks).  The combine of patches/ggml-m4/m4-kqkv.cu:314-338: m* = max m_s,
+// mla_merge.h -- the split-K merge of one unit (64 output columns of one head of one token), the
+// body of the PHASE merge kernel (mla_kernels.h describes the partial records).  The combine of patches/ggml-m4/m4-kqkv.cu:314-338: m* = max m_s,
 // l* = sum l_s e^(m_s - m*), o* = sum l_s e^(m_s - m*) (o_s / l_s), out = o* / l* (0 if every split
 // is empty).
 #pragma once
@@ -18,7 +17,7 @@ struct MergeScratch {
 };
 
 // One workgroup (256 threads) per unit: 8 column-lanes (8 f16 columns = 16 bytes
-// each) x 32 split-lanes.  Split-lane sl takes splits sl, sl + 32, ...: the loads of a 256-split
+// each) x 32 split-lanes (the record layout of mla_kernels.h).  Split-lane sl takes splits sl, sl + 32, ...: the loads of a 256-split
 // chunk (16 bytes of o/l plus m, l) all issue before the first use, then the chunk is folded with
 // the max taken first.  Split-lanes are combined with wavefront shuffles, then across the four
 // wavefronts through LDS.  Accumulators: (m, L = sum l_s e^(m_s - m), O = sum l_s e^(m_s - m) o_s).
@@ -34,8 +33,7 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
     const int c8 = tid & 7, sl_i = tid >> 3;               // column lane, split lane (0..31)
     const int c = cblk * 64 + 8 * c8;
     const int hh = h % PART_HEADS;
-    const size_t bb = part_block_bytes(dv, (int)sizeof(OT));
-    const char * base = part + ((size_t)(h / PART_HEADS) * nt + t) * n_split * bb;
+    const char * rec = part_record(part, h / PART_HEADS, nt, t, n_split, dv, (int)sizeof(OT));
     const int cc = min(c, dv - 8);
 
     float m = -INFINITY, L = 0.0f;
@@ -46,11 +44,12 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int s = s0 + 32 * j + sl_i;
-            const char * blk = base + (size_t)min(s, n_split - 1) * bb;
-            const float mv = reinterpret_cast<const float *>(blk)[hh];
-            ms[j] = (s < n_split) ? mv : -INFINITY;
-            ls[j] = reinterpret_cast<const float *>(blk)[PART_HEADS + hh];
-            const OT * src = reinterpret_cast<const OT *>(blk + 256) + (size_t)hh * dv + cc;
+            const int sc_ = min(s, n_split - 1);
+            // (m, l): consecutive split-lanes read consecutive pairs of this head's row
+            const f32x2 ml = *reinterpret_cast<const f32x2 *>(rec + part_ml_off(n_split, hh, sc_));
+            ms[j] = (s < n_split) ? ml[0] : -INFINITY;
+            ls[j] = ml[1];
+            const OT * src = reinterpret_cast<const OT *>(rec + part_o_off(n_split, sc_, dv, (int)sizeof(OT))) + (size_t)hh * dv + cc;
             if constexpr (sizeof(OT) == 2) {
                 const half8 v = *reinterpret_cast<const half8 *>(src);
 #pragma unroll

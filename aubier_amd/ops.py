@@ -268,19 +268,20 @@ def ggml_m4_phase_merge(part: torch.Tensor, out: Optional[torch.Tensor] = None, 
 
 
 def decode_partials(part, n_head: int, d_v: int = 512):
-    """Split a partial buffer (numpy/torch, [G, nt, S, 64 + 16 D_v] f32 words) into
+    """Split a partial buffer (numpy/torch, [G, nt, S, 64 + 16 D_v] f32 words; per (group, token)
+    one record: the (m, l) pairs [32 heads][S], then the o / l blocks [S][32 heads][D_v]) into
     m [H, nt, S], l [H, nt, S] and o_norm [H, nt, S, D_v] (float32 numpy arrays)."""
     import numpy as np
     p = part.detach().cpu().numpy() if isinstance(part, torch.Tensor) else np.asarray(part)
     G, nt, S, W = p.shape
-    m = p[..., :PART_HEADS]                                      # [G, nt, S, 32]
-    l = p[..., PART_HEADS:2 * PART_HEADS]
-    o = np.ascontiguousarray(p[..., 64:])
+    rec = np.ascontiguousarray(p).reshape(G, nt, S * W)
+    ml = rec[..., :2 * PART_HEADS * S].reshape(G, nt, PART_HEADS, S, 2)
+    o = np.ascontiguousarray(rec[..., 2 * PART_HEADS * S:])
     if W == part_floats(d_v, True):
         o = o.view(np.float16)
     o = o.reshape(G, nt, S, PART_HEADS, d_v)
-    m = np.moveaxis(m, 3, 1).reshape(G * PART_HEADS, nt, S)[:n_head]
-    l = np.moveaxis(l, 3, 1).reshape(G * PART_HEADS, nt, S)[:n_head]
+    m = np.moveaxis(ml[..., 0], 2, 1).reshape(G * PART_HEADS, nt, S)[:n_head]
+    l = np.moveaxis(ml[..., 1], 2, 1).reshape(G * PART_HEADS, nt, S)[:n_head]
     o = np.moveaxis(o, 3, 1).reshape(G * PART_HEADS, nt, S, d_v)[:n_head].astype(np.float32)
     return m, l, o
 

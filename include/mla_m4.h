@@ -67,15 +67,18 @@ enum {
     MLA_M4_PHASE_MERGE   = 2
 };
 
-/* Split-K partials.  One block per (32-head group g, token t, split s), blocks ordered
- * [g][t][s]:
- *   float m[32]          running max of the split's scaled, masked scores (natural-log units,
- *                        -INFINITY for a split with no live key)
- *   float l[32]          sum over the split's keys of exp(score - m)
- *   T     o[32][D_v]     o / l: the split's normalised softmax output (0 for an empty split);
- *                        T = f16 for an F16 cache (MLA_M4_PART_FLOATS(D_v) words per block),
- *                        T = f32 for an F32 cache (MLA_M4_PART_FLOATS_F32(D_v) words per block)
- * As a tensor: F32 ne [words per block, n_split, nt, ceil(H / 32)], contiguous. */
+/* Split-K partials.  One record per (32-head group g, token t), records ordered [g][t], of
+ * n_split * W words (W = MLA_M4_PART_FLOATS(D_v) for an F16 cache, MLA_M4_PART_FLOATS_F32(D_v)
+ * for an F32 cache):
+ *   float2 ml[32][n_split]      (m, l) of head h, split s at [h][s]:
+ *                               m  a reference for the split's scaled, masked scores (natural-log
+ *                                  units, at most 8 ln 2 below their max; -INFINITY for a split
+ *                                  with no live key) -- the merge only uses m + ln l
+ *                               l  sum over the split's keys of exp(score - m)
+ *   T      o[n_split][32][D_v]  o / l: the split's normalised softmax output (0 for an empty
+ *                               split); T = f16 for an F16 cache, f32 for an F32 cache
+ * As a tensor: F32 ne [W, n_split, nt, ceil(H / 32)], contiguous (its size; the words of a
+ * record are laid out as above). */
 #define MLA_M4_PART_HEADS 32
 #define MLA_M4_PART_FLOATS(dv) (64 + 16 * (dv))
 #define MLA_M4_PART_FLOATS_F32(dv) (64 + 32 * (dv))
