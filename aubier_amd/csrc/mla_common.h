@@ -32,8 +32,6 @@ __device__ __forceinline__ float exp2_unless(bool zero, float x) {
 // conversion ggml-cpu's mul_mat applies to src1 when src0 is F16.
 __device__ __forceinline__ half_t to_half(float x) { return (half_t)x; }
 
-// Cross-lane shuffles over the full 64-lane wavefront.
-__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, WAVE); }
 
 // Max / sum over the four 16-lane rows of a wavefront (lanes j, j + 16, j + 32, j + 48) with the
 // gfx950 row-swap instructions: v_permlane16_swap(x, x) leaves (row 0 | row 0 | row 2 | row 2) and
@@ -51,15 +49,63 @@ __device__ __forceinline__ float halves_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Lane l's partner l ^ k within rows of 16 lanes, by DPP (a VALU operand modifier, no LDS round
+// trip): k = 1, 2 quad_perm [1,0,3,2] / [2,3,0,1]; k = 4 row_half_mirror (l -> 7 - l within 8) then
+// quad_perm [3,2,1,0]; k = 8 row_ror:8.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int K>
+__device__ __forceinline__ float dpp_xor(float v) {
+    static_assert(K == 1 || K == 2 || K == 4 || K == 8, "row-local partners only");
+    if constexpr (K == 1) return dpp_mov<0xB1>(v);
+    else if constexpr (K == 2) return dpp_mov<0x4E>(v);
+    else if constexpr (K == 4) return dpp_mov<0x1B>(dpp_mov<0x141>(v));
+    else return dpp_mov<0x128>(v);
+}
+// (x of the even row, x of the odd row) of each pair of 16-lane rows / (low half, high half) of the
+// wavefront, at every lane: the operands of a symmetric combine of lanes l and l ^ 16 / l ^ 32
+__device__ __forceinline__ void rows_pair16(float v, float & even, float & odd) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    even = __uint_as_float(a[0]);
+    odd = __uint_as_float(a[1]);
+}
+__device__ __forceinline__ void halves_pair(float v, float & lo, float & hi) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(b[0]);
+    hi = __uint_as_float(b[1]);
+}
+
+// Butterflies over a 32-lane half (xor 16, 8, 4, 2, 1) and the whole wavefront (xor 32 first):
+// every step adds / maxes the partner's current value, as the LDS-permute loops would, on the VALU
+__device__ __forceinline__ float half_sum(float v) {
+    float e, o;
+    rows_pair16(v, e, o);
+    v = e + o;
+    v += dpp_xor<8>(v);
+    v += dpp_xor<4>(v);
+    v += dpp_xor<2>(v);
+    return v + dpp_xor<1>(v);
+}
+__device__ __forceinline__ float half_max(float v) {
+    float e, o;
+    rows_pair16(v, e, o);
+    v = fmaxf(e, o);
+    v = fmaxf(v, dpp_xor<8>(v));
+    v = fmaxf(v, dpp_xor<4>(v));
+    v = fmaxf(v, dpp_xor<2>(v));
+    return fmaxf(v, dpp_xor<1>(v));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor(v, o));
-    return v;
+    float lo, hi;
+    halves_pair(v, lo, hi);
+    return half_max(fmaxf(lo, hi));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += shfl_xor(v, o);
-    return v;
+    float lo, hi;
+    halves_pair(v, lo, hi);
+    return half_sum(lo + hi);
 }
 
 // gfx950 LDS transpose read (ds_read_b64_tr_b16).  In each 16-lane group, lane j supplies the

@@ -77,18 +77,40 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
         }
         m = mx;
     }
-    // fold the 8 split-lanes of this wavefront (lane bits 3..5)
-#pragma unroll
-    for (int off = 8; off < 64; off <<= 1) {
-        const float m2 = shfl_xor(m, off);
-        const float L2 = shfl_xor(L, off);
-        const float M = fmaxf(m, m2);
-        const float f1 = exp2_unless(m == -INFINITY, (m - M) * LOG2E);
+    // fold the 8 split-lanes of this wavefront (lane bits 3..5) without LDS round trips: the
+    // partner l ^ 8 by DPP, then the symmetric combine of the two 16-lane rows of each pair and of
+    // the two halves (v_permlane16_swap / v_permlane32_swap give both operands at every lane)
+    auto combine = [](float m1, float L1, const float (&O1)[8], float m2, float L2, const float (&O2)[8], float & mo,
+                      float & Lo, float (&Oo)[8]) {
+        const float M = fmaxf(m1, m2);
+        const float f1 = exp2_unless(m1 == -INFINITY, (m1 - M) * LOG2E);
         const float f2 = exp2_unless(m2 == -INFINITY, (m2 - M) * LOG2E);
-        L = L * f1 + L2 * f2;
+        Lo = L1 * f1 + L2 * f2;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) O[k] = O[k] * f1 + shfl_xor(O[k], off) * f2;
-        m = M;
+        for (int k = 0; k < 8; ++k) Oo[k] = O1[k] * f1 + O2[k] * f2;
+        mo = M;
+    };
+    {
+        float O2[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) O2[k] = dpp_xor<8>(O[k]);
+        combine(m, L, O, dpp_xor<8>(m), dpp_xor<8>(L), O2, m, L, O);
+    }
+    {
+        float ma, mb, La, Lb, Oa[8], Ob[8];
+        rows_pair16(m, ma, mb);
+        rows_pair16(L, La, Lb);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) rows_pair16(O[k], Oa[k], Ob[k]);
+        combine(ma, La, Oa, mb, Lb, Ob, m, L, O);
+    }
+    {
+        float ma, mb, La, Lb, Oa[8], Ob[8];
+        halves_pair(m, ma, mb);
+        halves_pair(L, La, Lb);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) halves_pair(O[k], Oa[k], Ob[k]);
+        combine(ma, La, Oa, mb, Lb, Ob, m, L, O);
     }
     if (lane < 8) {
         sm[w][c8] = m;

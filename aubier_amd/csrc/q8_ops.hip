@@ -30,9 +30,7 @@ __device__ __forceinline__ uint32_t bytes4(const uint32_t * D, int B) {
 // inside the half): returns the int8 quant, d16 = the block's f16 scale as f32.
 template <bool DIV>
 __device__ __forceinline__ int quant_lane(float x, float & d16) {
-    float amax = fabsf(x);
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float amax = half_max(fabsf(x));
     const float d = amax / 127.0f;
     d16 = round_to_f16(d);
     if constexpr (DIV) return amax == 0.0f ? 0 : (int)roundf(x / d);
@@ -40,12 +38,9 @@ __device__ __forceinline__ int quant_lane(float x, float & d16) {
     return (int)roundf(x * id);
 }
 
-// The 32-lane butterfly of warp_reduce_sum (xor 16, 8, 4, 2, 1) inside a half-wavefront.
-__device__ __forceinline__ float half_wave_sum(float v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+// The 32-lane butterfly of warp_reduce_sum (xor 16, 8, 4, 2, 1) inside a half-wavefront: the
+// same additions in the same order (mla_common.h).
+__device__ __forceinline__ float half_wave_sum(float v) { return half_sum(v); }
 
 // ---- WKB, Q8_0 W_kb: one workgroup per (head, token); a thread per output row ----
 // The head's d_n activations are quantised once into LDS (4 int8 per word); each row's blocks

@@ -20,6 +20,7 @@ constexpr int WKB_NI = 4;   // row loads in flight per wavefront
 template <int DN>
 __global__ __launch_bounds__(256) void wkb_f32_kernel(WkbArgs a) {
     constexpr int LPR = DN / 4;          // lanes per row
+    static_assert(LPR == 16 || LPR == 32, "rows of one or two 16-lane DPP rows");
     constexpr int RPI = 64 / LPR;        // rows per load instruction
     constexpr int RPW = RPI * WKB_NI;    // rows per wavefront
     const int lane = threadIdx.x & 63;
@@ -47,10 +48,19 @@ __global__ __launch_bounds__(256) void wkb_f32_kernel(WkbArgs a) {
             v = fmaf(wv[i][3], qv.w, v);
             p[i] = v;
         }
+        // sum over the row's LPR lanes: the 16-lane rows by DPP, then (d_n = 128) the row pair
 #pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1)
-#pragma unroll
-            for (int i = 0; i < WKB_NI; ++i) p[i] += shfl_xor(p[i], off);
+        for (int i = 0; i < WKB_NI; ++i) {
+            p[i] += dpp_xor<8>(p[i]);
+            p[i] += dpp_xor<4>(p[i]);
+            p[i] += dpp_xor<2>(p[i]);
+            p[i] += dpp_xor<1>(p[i]);
+            if constexpr (LPR == 32) {
+                float e, o;
+                rows_pair16(p[i], e, o);
+                p[i] = e + o;
+            }
+        }
         if (li == 0) {
             char * drow = reinterpret_cast<char *>(a.dst) + (size_t)t * a.d_nb2 + (size_t)h * a.d_nb1;
 #pragma unroll
