@@ -207,8 +207,9 @@ __device__ __forceinline__ void stage_q(const DecodeArgs & a, const SliceStream<
 // of their MFMAs; the scheduling barriers keep the compiler from sinking them back next to their
 // use.  Two accumulator chains per head tile (even / odd steps) keep consecutive MFMAs
 // independent.  Returns with the slice's mask slot landed.  WAIT = false: the slice is known to
-// be in LDS already (no DMA accounting, no next-slice DMA).
-template <int DK, bool DMA, bool WAIT = true>
+// be in LDS already (no DMA accounting, no next-slice DMA).  NT: the cache policy of the next
+// slice's DMA (streaming for decode; cached where other workgroups re-read the cache).
+template <int DK, bool DMA, bool WAIT = true, bool NT = true>
 __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const SliceDma & dn, const char * sb, int lane,
                                          const half8 (&qreg)[2][SliceGeom<DK>::QSTEPS], f32x4 & s0, f32x4 & s1) {
     static_assert(WAIT || !DMA, "a slice already in LDS comes with no DMA to spread");
@@ -242,11 +243,11 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc1, 0, 0, 0);
         }
-        if constexpr (DMA) ss.put(dn, s);
+        if constexpr (DMA) ss.template put<NT>(dn, s);
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (DMA) {
-        ss.put(dn, G::DMA_N);
+        ss.template put<NT>(dn, G::DMA_N);
         wait_vm<G::DMA_N + 1>();             // the mask slot (the next slice's DMA_N + 1 may be in flight)
     } else if constexpr (WAIT) {
         wait_vm<0>();

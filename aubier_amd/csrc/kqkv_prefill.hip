@@ -12,7 +12,7 @@
 //     LDS ring (decode_common.h layout, cached DMA: the cache is re-read by every token group and
 //     stays in L2 / MALL) plus its own token's 64 mask values, and then every wave runs all four
 //     slices -- 4 tokens x 32 heads share each K / V byte read from LDS.  One workgroup barrier
-//     per tile; the next tile's DMA is issued right after it.
+//     per tile; the next tile's DMA goes out one instruction per Q.K^T step of the first slice.
 //   * Per slice: S^T = K . Q^T (16 keys x 32 heads, v_mfma_f32_16x16x32_f16), scores with the
 //     token's mask, a lazily moved reference max (P = exp2(s - m) <= 256), P^T for P.V by two
 //     v_permlane16_swap, o^T += V^T . P^T (v_mfma_f32_32x32x16_f16, V^T by ds_read_b64_tr_b16).
@@ -56,20 +56,24 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
     const bool token_live = t_w < a.nt;
     const int t = min(t_w, a.nt - 1);                // (a wave past the last token mirrors it, unused)
 
-    const SliceStream<DK> ss(a, sp, t, w, lds_addr(ring), lane);
+    SliceStream<DK> ss(a, sp, t, w, lds_addr(ring), lane);
+    ss.mvoff = 4u * (uint32_t)lane;                  // the mask slot holds this token's 64 keys of the tile
     const int n_my = ss.n_my;
-    // DMA of tile k into stage s: this wave's 16-key slice of K rows (cached policy) and this
-    // wave's token's mask over the tile's 64 keys (zeros past n_kv or without a mask)
-    auto issue = [&](int s, int k) {
-        const SliceDma d = ss.plan(s, k);
+    // DMA of tile k into stage s: this wave's 16-key slice of K rows (cached policy: every token
+    // group re-reads the cache) and this wave's token's mask over the tile's 64 keys (zeros past
+    // n_kv or without a mask)
+    auto plan = [&](int s, int k) {
+        SliceDma d = ss.plan(s, k);
         const int tile = min(ss.t0 + min(k, n_my - 1), ss.n_tiles - 1);
         const int mleft = a.n_kv - tile * TK;
-        const i32x4 mrs = make_rsrc(ss.mrow + tile * TK, (ss.has_mask && mleft > 0) ? (uint32_t)mleft * 4u : 0u);
-#pragma unroll
-        for (int i = 0; i < G::DMA_N; ++i) ss.template put<false>(d, i);
-        dma4(mrs, 4u * (uint32_t)lane, 0u, d.sb + (uint32_t)G::ROWS_BYTES);
+        d.mrs = make_rsrc(ss.mrow + tile * TK, (ss.has_mask && mleft > 0) ? (uint32_t)mleft * 4u : 0u);
+        return d;
     };
-    issue(0, 0);
+    {
+        const SliceDma d0 = plan(0, 0);
+#pragma unroll
+        for (int i = 0; i <= G::DMA_N; ++i) ss.template put<false>(d0, i);
+    }
 
     // ---- q fragments of this wave's token: qreg[n][s] = head 16 n + j16, d = 32 s + 8 g .. +7 ----
     half8 qreg[2][G::QSTEPS];
@@ -115,7 +119,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
     for (int k = 0; k < n_my; ++k) {
         wait_vm<0>();                        // this wave's slot of tile k (and its mask row) has landed
         __syncthreads();                     // all four have; every wave is done with tile k - 1
-        if (k + 1 < n_my) issue((k + 1) & 1, k + 1);
+        // tile k + 1's DMA goes out one instruction per Q.K^T step of the first slice (issued in
+        // one block it stalls the wave for ~1,400 cycles)
+        const bool pf = k + 1 < n_my;
+        const SliceDma dn = plan((k + 1) & 1, k + 1);
         const int par = k & 1;
         const int key_t = (ss.t0 + k) * TK;
         const char * mkb = ring + ss.stage_off(par, w) + G::ROWS_BYTES;    // this token's mask, 64 keys
@@ -123,7 +130,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
         for (int ks = 0; ks < NWAVE; ++ks) {
             const char * sb = ring + ss.stage_off(par, ks);
             f32x4 s0, s1;
-            qk_slice<DK, false, false>(ss, none, sb, lane, qreg, s0, s1);
+            if (ks == 0 && pf) qk_slice<DK, true, true, false>(ss, dn, sb, lane, qreg, s0, s1);
+            else qk_slice<DK, false, false>(ss, none, sb, lane, qreg, s0, s1);
             const f32x4 mk = *reinterpret_cast<const f32x4 *>(mkb + 64 * ks + 16 * g);
             float sc[2][4], mx[2];
             slice_scores(a, mk, key_t + WK * ks, lane, s0, s1, sc, mx);
