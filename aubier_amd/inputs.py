@@ -136,3 +136,25 @@ def make_config(cfg: int, n_kv: Optional[int] = None, nt: Optional[int] = None) 
     w_kb = randn(sd["w_kb"], N_HEAD * D_V * D_NOPE).reshape(N_HEAD, D_V, D_NOPE)
     return MlaInputs(cfg=cfg, n_kv=W, n_live=L, nt=T, kc_f16=f16, kcache=kcache, q_nope=q_nope, q_pe=q_pe,
                      w_kb=w_kb, mask=mask, seeds=sd, notes=notes)
+
+
+def make_batch(n_seq: int, region: int, lens: Optional[list] = None, seed_cfg: int = 6) -> MlaInputs:
+    """Batch-of-N decode (the engine's per-sequence regions, m1_layer.h:212-223 / m1_session.h:188-201):
+    one cache window of width n_seq * region, sequence s owning cells [s * region, (s + 1) * region);
+    row s's mask is 0 on [s * region, s * region + len_s) and -inf elsewhere.  len_s is seeded in
+    [1, region] unless given.  Cache values, q and W_kb as config 2 (f16 cache, N(0,1) * 0.05)."""
+    W = n_seq * region
+    sd = {k: seed_of(seed_cfg, i) for i, k in enumerate(["kcache", "q_nope", "q_pe", "w_kb", "aux"])}
+    if lens is None:
+        r = splitmix_u64(sd["aux"], n_seq)
+        lens = [1 + int(r[i] % np.uint64(region)) for i in range(n_seq)]
+    assert len(lens) == n_seq and all(1 <= l <= region for l in lens)
+    mask = np.full((n_seq, W), -np.inf, dtype=np.float32)
+    for i, l in enumerate(lens):
+        mask[i, i * region:i * region + l] = 0.0
+    kcache = randn(sd["kcache"], W * D_K).reshape(W, D_K).astype(np.float16)
+    q_nope = randn(sd["q_nope"], n_seq * N_HEAD * D_NOPE).reshape(n_seq, N_HEAD, D_NOPE)
+    q_pe = randn(sd["q_pe"], n_seq * N_HEAD * D_ROPE).reshape(n_seq, N_HEAD, D_ROPE)
+    w_kb = randn(sd["w_kb"], N_HEAD * D_V * D_NOPE).reshape(N_HEAD, D_V, D_NOPE)
+    return MlaInputs(cfg=seed_cfg, n_kv=W, n_live=max(lens), nt=n_seq, kc_f16=True, kcache=kcache, q_nope=q_nope,
+                     q_pe=q_pe, w_kb=w_kb, mask=mask, seeds=sd, notes=f"{n_seq} sequences x {region} cells, lens {lens}")
