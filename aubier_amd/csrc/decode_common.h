@@ -137,6 +137,76 @@ struct SliceStream {
     }
 };
 
+constexpr int SHORT_MAX_TILES = 6;   // longest split of the barrier-per-tile kernel
+constexpr int ROWS_MAX = 16;         // rows (tokens) per workgroup of the decode kernels
+
+// Workgroups along the row axis of a decode launch: rows t = z, z + Z, ... share a workgroup, Z as
+// small as keeps ~256 workgroups in flight (one, at 256 splits: batch-of-N decode over per-sequence
+// regions then has one live row per split), and at most ROWS_MAX rows per workgroup.
+inline int decode_row_groups(const DecodeArgs & a, int n_hgroups) {
+    const int per_row = a.n_split * n_hgroups;
+    int z = (256 + per_row - 1) / per_row;
+    z = z < 1 ? 1 : z;
+    const int zmin = (a.nt + ROWS_MAX - 1) / ROWS_MAX;
+    z = z < zmin ? zmin : z;
+    return z < a.nt ? z : a.nt;
+}
+
+// Liveness of this workgroup's rows in split sp: bit i set when row blockIdx.z + i gridDim.z has a
+// key with mask > -inf below n_kv in the split (splits of at most MAXT tiles).  Wave w checks rows
+// w, w + 4, w + 8, w + 12; every load is issued before the first compare (one round trip).
+template <int MAXT>
+__device__ __forceinline__ uint32_t live_rows_of_wave(const DecodeArgs & a, int sp, int w, int lane) {
+    constexpr int RW = ROWS_MAX / NWAVE;
+    const int base_t = a.n_tiles / a.n_split, rem = a.n_tiles % a.n_split;
+    const int t0 = sp * base_t + min(sp, rem);
+    const int n_my = base_t + (sp < rem ? 1 : 0);
+    const int k0 = t0 * TK, k1 = min((t0 + n_my) * TK, a.n_kv);
+    float v[RW][MAXT];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int t = (int)blockIdx.z + (w + NWAVE * r) * (int)gridDim.z;
+        const float * row = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) +
+                                                            (size_t)min(t, a.nt - 1) * a.mask_nb1);
+#pragma unroll
+        for (int j = 0; j < MAXT; ++j) {
+            const int k = k0 + lane + 64 * j;
+            v[r][j] = (t < a.nt && k < k1) ? row[k] : -INFINITY;
+        }
+    }
+    uint32_t bits = 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        bool live = false;
+#pragma unroll
+        for (int j = 0; j < MAXT; ++j) live |= v[r][j] != -INFINITY;
+        if (__builtin_amdgcn_ballot_w64(live) != 0) bits |= 1u << (w + NWAVE * r);
+    }
+    return bits;
+}
+
+// Whether token t has a live key (mask > -inf, key < n_kv) in the split's tiles: the mask row
+// read over the split's range (cached loads, one key per lane per step), OR-ed over the wavefront.
+// Every wave of the workgroup computes the same answer.  Without a mask every key below n_kv is live.
+template <int DK>
+__device__ __forceinline__ bool split_live(const DecodeArgs & a, const SliceStream<DK> & ss, int t, int lane) {
+    const int k0 = ss.t0 * TK, k1 = min((ss.t0 + ss.n_my) * TK, a.n_kv);
+    if (a.mask == nullptr) return k0 < k1;
+    const float * row = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) + (size_t)t * a.mask_nb1);
+    bool live = false;
+    for (int k = k0 + lane; k < k1; k += 64) live |= row[k] != -INFINITY;
+    return __builtin_amdgcn_ballot_w64(live) != 0;
+}
+
+// The (m, l) pairs of a split with no live key: m = -inf, l = 0 for the record's 32 heads; its o
+// block is left unwritten (the merge reads o only where m > -inf).  Lanes 0..31 of one wave.
+__device__ __forceinline__ void write_empty_pairs(const DecodeArgs & a, int g, int t, int sp, int dv, int lane) {
+    if (lane < HG) {
+        char * rec = part_record(a.part, g, a.nt, t, a.n_split, dv, 2);
+        *reinterpret_cast<f32x2 *>(rec + part_ml_off(a.n_split, lane, sp)) = f32x2{-INFINITY, 0.0f};
+    }
+}
+
 // q block (32 heads x DK f32) -> stage 1 of the ring by DMA, tile 0's slice -> stage 0 behind it,
 // then f16 B fragments in registers: qreg[n][s] = head 16 n + j16, d = 32 s + 8 g .. +7.  Staging
 // slot of f32 chunk c (4 floats) of head h: h * QC + (c ^ (h & 15)), so the fragment reads (16

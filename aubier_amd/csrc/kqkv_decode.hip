@@ -49,20 +49,28 @@ struct ShortCfg {
     static_assert(NWAVE * NTQ - 1 < 64, "P.V operand offsets fit the DS immediate");
 };
 
+// LDS of the kernel: the slice ring, the P exchange and the slice maxima, by tile parity
 template <int DK, int DV>
-__global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) {
+struct ShortLds {
+    __attribute__((aligned(16))) char ring[SliceGeom<DK>::RING];       // [stage][wave] K rows + mask
+    __attribute__((aligned(16))) half_t px[2][HG * ShortCfg<DK, DV>::PROW];
+    __attribute__((aligned(16))) float red[2][HG][NWAVE];              // [head][wave]
+};
+
+// One row (token) t of the split: the whole pass, from the q staging to the partial record.
+template <int DK, int DV>
+__device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds<DK, DV> & sh) {
     using G = SliceGeom<DK>;
     using C = ShortCfg<DK, DV>;
-    __shared__ __attribute__((aligned(16))) char ring[G::RING];          // [stage][wave] K rows + mask
-    __shared__ __attribute__((aligned(16))) half_t px[2][HG * C::PROW];  // P exchange, by tile parity
-    __shared__ __attribute__((aligned(16))) float red[2][HG][NWAVE];     // slice maxima [head][wave], by tile parity
+    char (&ring)[G::RING] = sh.ring;
+    half_t (&px)[2][HG * C::PROW] = sh.px;
+    float (&red)[2][HG][NWAVE] = sh.red;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sp = blockIdx.x;
     const int hg0 = blockIdx.y * HG;
-    const int t = blockIdx.z;
     const int g = lane >> 4;                 // 16-lane group
     const int j16 = lane & 15;
 
@@ -244,24 +252,59 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     }
 }
 
+// ROWS = false: row blockIdx.z (one token, the plain decode step).  ROWS = true: rows blockIdx.z,
+// blockIdx.z + gridDim.z, ... of split blockIdx.x (batch-of-N decode puts every row of the split in
+// one workgroup); with a mask, the rows that hold no live key of the split (per-sequence regions)
+// are found first, in one round trip, and only record an empty split; the others run the whole
+// pass in turn.
+template <int DK, int DV, bool ROWS>
+__global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) {
+    __shared__ ShortLds<DK, DV> sh;
+    if constexpr (!ROWS) {
+        decode_row<DK, DV>(a, blockIdx.z, sh);
+        return;
+    }
+    __shared__ uint32_t live_w[NWAVE];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint32_t live = ~0u;
+    if (a.nt > 1 && a.dst == nullptr && a.mask != nullptr) {
+        const uint32_t bits = live_rows_of_wave<SHORT_MAX_TILES>(a, blockIdx.x, w, lane);
+        if (lane == 0) live_w[w] = bits;
+        __syncthreads();
+        live = live_w[0] | live_w[1] | live_w[2] | live_w[3];
+    }
+    int i = 0;
+    for (int t = blockIdx.z; t < a.nt; t += gridDim.z, ++i) {
+        if (!((live >> i) & 1u)) {
+            if (w == 0) write_empty_pairs(a, blockIdx.y, t, blockIdx.x, DV, lane);
+            continue;
+        }
+        decode_row<DK, DV>(a, t, sh);
+        __syncthreads();                     // the next row's q staging reuses the ring
+    }
+}
+
 }  // namespace
 
 template <int DK, int DV>
 static hipError_t launch_short(const DecodeArgs & a, int n_hgroups, hipStream_t stream) {
-    dim3 grid(a.n_split, n_hgroups, a.nt);
-    hipLaunchKernelGGL((kqkv_decode_f16_kernel<DK, DV>), grid, dim3(NTHR), 0, stream, a);
+    if (a.nt == 1)
+        hipLaunchKernelGGL((kqkv_decode_f16_kernel<DK, DV, false>), dim3(a.n_split, n_hgroups, 1), dim3(NTHR), 0, stream, a);
+    else
+        hipLaunchKernelGGL((kqkv_decode_f16_kernel<DK, DV, true>), dim3(a.n_split, n_hgroups, decode_row_groups(a, n_hgroups)),
+                           dim3(NTHR), 0, stream, a);
     return hipGetLastError();
 }
 
 hipError_t launch_kqkv_decode_f16_long(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
 
-// Splits of at most LONG_TILES tiles take the barrier-per-tile kernel above (short tail); longer
-// ones the independent-wave kernel of kqkv_decode_long.hip (no barrier in the loop, costlier end).
-constexpr int LONG_TILES = 6;
-
+// Splits of at most SHORT_MAX_TILES tiles take the barrier-per-tile kernel above (short tail);
+// longer ones the independent-wave kernel of kqkv_decode_long.hip (no barrier in the loop,
+// costlier end).
 hipError_t launch_kqkv_decode_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream) {
     const int tiles_per_split = (a.n_tiles + a.n_split - 1) / a.n_split;
-    if (tiles_per_split > LONG_TILES) return launch_kqkv_decode_f16_long(dk, dv, a, stream);
+    if (tiles_per_split > SHORT_MAX_TILES) return launch_kqkv_decode_f16_long(dk, dv, a, stream);
     const int n_hgroups = (a.n_head + decode::HG - 1) / decode::HG;
     if (dk == 576 && dv == 512) return launch_short<576, 512>(a, n_hgroups, stream);
     if (dk == 320 && dv == 256) return launch_short<320, 256>(a, n_hgroups, stream);

@@ -57,6 +57,12 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
 
     const SliceStream<DK> ss(a, sp, t, w, lds_addr(ring), lane);
     const int n_my = ss.n_my;
+    // several rows (batch-of-N decode over per-sequence regions): a split that holds no live key
+    // of this row only records that, before any DMA
+    if (a.nt > 1 && a.dst == nullptr && !split_live<DK>(a, ss, t, lane)) {
+        if (w == 0) write_empty_pairs(a, blockIdx.y, t, sp, DV, lane);
+        return;
+    }
     half8 qreg[2][G::QSTEPS];
     stage_q<DK>(a, ss, ring, hg0, t, lane, qreg);
 

@@ -176,6 +176,7 @@ __global__ __launch_bounds__(256) void merge_few_kernel(const char * __restrict_
     for (int s = 0; s < n_split; ++s) {
         const float f = ls[s] * exp2_unless(ms[s] == -INFINITY, (ms[s] - m) * LOG2E);
         L += f;
+        if (ms[s] == -INFINITY) continue;   // an empty split's o block is never written
         const OT * src = reinterpret_cast<const OT *>(rec + part_o_off(n_split, s, dv, (int)sizeof(OT))) + (size_t)hh * dv + 8 * c8;
         if constexpr (sizeof(OT) == 2) {
             const half8 v = *reinterpret_cast<const half8 *>(src);

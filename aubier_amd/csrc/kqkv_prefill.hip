@@ -69,6 +69,15 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
         d.mrs = make_rsrc(ss.mrow + tile * TK, (ss.has_mask && mleft > 0) ? (uint32_t)mleft * 4u : 0u);
         return d;
     };
+    // Rows over per-sequence regions (batch-of-N decode): a wave whose token has no live key in this
+    // split still streams its slices for the others but computes nothing; a workgroup with no live
+    // token records empty splits and leaves before any DMA.  (One split writes dst directly: every
+    // row is computed.)
+    const bool live_w = token_live && (a.dst != nullptr || split_live<DK>(a, ss, t, lane));
+    if (!__syncthreads_or(live_w)) {
+        if (token_live && a.dst == nullptr) write_empty_pairs(a, blockIdx.y, t, sp, DV, lane);
+        return;
+    }
     {
         const SliceDma d0 = plan(0, 0);
 #pragma unroll
@@ -126,6 +135,13 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
         const int par = k & 1;
         const int key_t = (ss.t0 + k) * TK;
         const char * mkb = ring + ss.stage_off(par, w) + G::ROWS_BYTES;    // this token's mask, 64 keys
+        if (!live_w) {                       // only this wave's slice of the next tile
+            if (pf) {
+#pragma unroll
+                for (int i = 0; i <= G::DMA_N; ++i) ss.template put<false>(dn, i);
+            }
+            continue;
+        }
 #pragma unroll 1
         for (int ks = 0; ks < NWAVE; ++ks) {
             const char * sb = ring + ss.stage_off(par, ks);
@@ -202,6 +218,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
     const float L = halves_sum(l_acc);         // head hl, all keys of the split
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     if (!token_live) return;
+    if (!live_w) {                           // (a.dst == nullptr here)
+        write_empty_pairs(a, blockIdx.y, t, sp, DV, lane_e);
+        return;
+    }
     const int hi4 = 4 * (lane_e >> 5);
     if (a.dst != nullptr) {                  // single split: o / l in f32 straight to dst
         const int h = hg0 + hl;

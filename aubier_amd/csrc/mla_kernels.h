@@ -17,8 +17,9 @@ namespace mla {
 //          running reference at most 8 ln 2 below it (MFMA kernels); -inf if the split is empty.
 //          The merge only uses m + ln l.
 //   l      sum_j exp(s_j - m)
-//   o / l  the split's normalised softmax output, 0 for an empty split.  T is the cache's element
-//          type: f16 for an f16 cache (|o / l| <= max|V|, so it cannot overflow), f32 for f32.
+//   o / l  the split's normalised softmax output.  T is the cache's element type: f16 for an f16
+//          cache (|o / l| <= max|V|, so it cannot overflow), f32 for f32.  A split with no live
+//          key (m = -inf) may leave its block unwritten; the merge never reads it.
 constexpr int PART_HEADS = 32;
 __host__ __device__ constexpr size_t part_block_bytes(int dv, int o_bytes) {
     return 256 + (size_t)PART_HEADS * (size_t)o_bytes * (size_t)dv;
@@ -54,9 +55,11 @@ struct DecodeArgs {
 };
 
 hipError_t launch_kqkv_decode_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
-// several query tokens (nt >= PREFILL_MIN_TOKENS): 4 tokens per workgroup sharing each K / V tile;
-// grid (n_split, ceil(H/32), ceil(nt/4)); same outputs and geometries as the decode kernel
-constexpr int PREFILL_MIN_TOKENS = 4;
+// several query tokens (nt >= PREFILL_MIN_TOKENS, chunked prefill): 4 tokens per workgroup sharing
+// each K / V tile; grid (n_split, ceil(H/32), ceil(nt/4)); same outputs and geometries as the
+// decode kernel.  Fewer rows (batch-of-N decode, often over disjoint per-sequence regions) stay on
+// the decode kernels, whose workgroups skip the rows a split holds no live key of.
+constexpr int PREFILL_MIN_TOKENS = 16;
 constexpr int PREFILL_TOKENS_PER_WG = 4;
 hipError_t launch_kqkv_prefill_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
 bool decode_f16_supported(int dk, int dv);

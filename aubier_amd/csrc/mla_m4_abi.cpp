@@ -123,7 +123,9 @@ int default_splits(const KqkvShape & s) {
     if (use_prefill(s))
         groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) *
                  ((s.nt + mla::PREFILL_TOKENS_PER_WG - 1) / mla::PREFILL_TOKENS_PER_WG);
-    else if (use_mfma(s)) groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) * s.nt;
+    // decode kernels: the rows of a split share its workgroup (the launch adds row groups only
+    // when there are few splits), so the split count is the single-row one
+    else if (use_mfma(s)) groups = (s.n_head + DECODE_HEADS - 1) / DECODE_HEADS;
     else groups = s.n_head * s.nt;
     int64_t sp = (TARGET_WG + groups - 1) / groups;
     if (sp > tiles) sp = tiles;

@@ -35,6 +35,12 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
     const int hh = h % PART_HEADS;
     const char * rec = part_record(part, h / PART_HEADS, nt, t, n_split, dv, (int)sizeof(OT));
     const int cc = min(c, dv - 8);
+    // the record's o blocks, read through a buffer resource: an empty split's block (never
+    // written) is skipped by an out-of-range offset, which reads zeros without a memory access
+    const char * obase = rec + part_o_off(n_split, 0, dv, (int)sizeof(OT));
+    const uint32_t oblk = (uint32_t)(PART_HEADS * dv * (int)sizeof(OT));
+    const uint32_t orecs = (uint32_t)n_split * oblk;
+    const uint32_t ocol = (uint32_t)((hh * dv + cc) * (int)sizeof(OT));
 
     float m = -INFINITY, L = 0.0f;
     float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -49,14 +55,15 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
             const f32x2 ml = *reinterpret_cast<const f32x2 *>(rec + part_ml_off(n_split, hh, sc_));
             ms[j] = (s < n_split) ? ml[0] : -INFINITY;
             ls[j] = ml[1];
-            const OT * src = reinterpret_cast<const OT *>(rec + part_o_off(n_split, sc_, dv, (int)sizeof(OT))) + (size_t)hh * dv + cc;
+            // o only where the split has a live key
+            const uint32_t off = (ms[j] != -INFINITY) ? (uint32_t)sc_ * oblk + ocol : 0xFFFFFFE0u;   // (+16 stays out of range)
             if constexpr (sizeof(OT) == 2) {
-                const half8 v = *reinterpret_cast<const half8 *>(src);
+                const half8 v = __builtin_bit_cast(half8, buf_ld16(obase, orecs, off));
 #pragma unroll
                 for (int k = 0; k < 8; ++k) os[j][k] = (float)v[k];
             } else {
-                const f32x4 v0 = *reinterpret_cast<const f32x4 *>(src);
-                const f32x4 v1 = *reinterpret_cast<const f32x4 *>(src + 4);
+                const f32x4 v0 = __builtin_bit_cast(f32x4, buf_ld16(obase, orecs, off));
+                const f32x4 v1 = __builtin_bit_cast(f32x4, buf_ld16(obase, orecs, off + 16u));
 #pragma unroll
                 for (int k = 0; k < 4; ++k) { os[j][k] = v0[k]; os[j][4 + k] = v1[k]; }
             }

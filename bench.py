@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--splits", type=int, default=0, help="split count (0 = library default)")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="batch-of-N decode: N rows, each over its own 32768/N-cell region of one window")
     ap.add_argument("--sweep", action="store_true", help="also time S in {64,128,192,256}")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm", action="store_true", help="also report WARM (one cache) timings")
@@ -67,9 +69,13 @@ def main() -> int:
     A.load_library()
     if args.ops:
         return ops_bench(args)
-    inp = I.make_config(args.config)
-    if inp.nt > 1:
-        return prefill_bench(args, inp)
+    if args.batch:
+        region = 32768 // args.batch
+        inp = I.make_batch(args.batch, region, lens=[region] * args.batch)
+    else:
+        inp = I.make_config(args.config)
+        if inp.nt > 1:
+            return prefill_bench(args, inp)
     H, DV, DK = I.N_HEAD, I.D_V, I.D_K
     W = inp.n_kv
     es = 2 if inp.kc_f16 else 4
@@ -228,7 +234,9 @@ def main() -> int:
         "metric": METRIC, "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1000.0, 6), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16" if inp.kc_f16 else "f32", "data": "synthetic",
-        "config": {"workload": f"config {args.config}: MLA decode, 1 token x 32 heads, {W} keys, "
+        "config": {"workload": (f"batch-of-{inp.nt} decode: {inp.nt} rows x 32 heads, each over its own "
+                                f"{W // inp.nt}-cell region of one {W}-cell window, " if args.batch else
+                                f"config {args.config}: MLA decode, 1 token x 32 heads, {W} keys, ") +
                                f"{'f16' if inp.kc_f16 else 'f32'} latent+rope cache [{W},576], W_kb f32 [32,512,128], "
                                f"split-K S={S} + PHASE merge, COLD ({N_ROT} rotating copies), hipGraph",
                    "n_kv": W, "n_head": H, "d_k": DK, "d_v": DV, "splits": S, "seeds": inp.seeds, "notes": inp.notes},

@@ -75,8 +75,10 @@ enum {
  *                                  units, at most 8 ln 2 below their max; -INFINITY for a split
  *                                  with no live key) -- the merge only uses m + ln l
  *                               l  sum over the split's keys of exp(score - m)
- *   T      o[n_split][32][D_v]  o / l: the split's normalised softmax output (0 for an empty
- *                               split); T = f16 for an F16 cache, f32 for an F32 cache
+ *   T      o[n_split][32][D_v]  o / l: the split's normalised softmax output; T = f16 for an
+ *                               F16 cache, f32 for an F32 cache.  A split with no live key
+ *                               (m = -INFINITY) may leave its block unwritten: the merge never
+ *                               reads it
  * As a tensor: F32 ne [W, n_split, nt, ceil(H / 32)], contiguous (its size; the words of a
  * record are laid out as above). */
 #define MLA_M4_PART_HEADS 32

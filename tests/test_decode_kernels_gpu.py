@@ -108,8 +108,8 @@ def test_short_and_long_kernels_agree_with_oracle(dev, dk, dv, n_kv, splits, sha
 
 
 @pytest.mark.parametrize("dk,dv,n_kv,nt,splits", [
-    (576, 512, 3000, 6, (None, 1, 3)),      # a full 4-token group and a partial one
-    (320, 256, 2000, 9, (None, 2)),
+    (576, 512, 3000, 18, (None, 1, 3)),     # full 4-token groups and a partial one
+    (320, 256, 2000, 17, (None, 2)),
 ])
 @pytest.mark.parametrize("q_scale", [0.05, 1.0])
 def test_prefill_kernel_causal(dev, dk, dv, n_kv, nt, splits, q_scale):
