@@ -1,7 +1,7 @@
 // kqkv_prefill.hip -- GGML_OP_M4_KQKV for several query tokens (chunked prefill), on MFMA.
 //
 // The op of patches/ggml-m4/m4-kqkv.cu:340-378 (which the reference only runs for one token) for
-// nt >= 4 tokens: out[h, t] = softmax_j(kq_scale q[t, h] . K[j] + mask[t, j]) . V[j] over the
+// nt >= 16 tokens: out[h, t] = softmax_j(kq_scale q[t, h] . K[j] + mask[t, j]) . V[j] over the
 // cache.  With many tokens the work is a dense contraction (config 5: 285 GFLOP over a 9.4 MB
 // cache), so the design is MFMA-bound rather than HBM-bound:
 //   * One workgroup per (split, 32-head group, 4 tokens); wave w owns token 4 z + w with all 32
