@@ -43,16 +43,17 @@ struct SliceGeom {
 
 // Slot layout (one wave slice, 16 cache rows of CH 16-byte chunks): 1 KB blocks b = 0 .. CH/4 - 1,
 // block b holding rows 8 (b & 1) .. +7 and chunks 8 (b >> 1) .. +7 -- one 128-byte segment of each
-// of 8 rows.  Row r, chunk c of the block sits at slot 16 ((r & 7) >> 1) + 8 (r & 1) + (c ^ row_sw(r)).
-// DMA instruction b fills block b (lane l -> slot l), so quarter-wave qq fetches rows 2 qq, 2 qq + 1
-// as two whole 128-byte segments: whole cache lines per request (a layout that splits each line over
-// two instructions streams ~20% slower per CU).  The swizzle keeps on distinct banks, at 128 and 256
-// bytes per LDS clock alike, both the Q.K^T reads (16 rows, one chunk) and the transpose reads of
-// P.V (4 rows x 2 chunks per 16 lanes, 4 rows x 4 chunks per 32 lanes).  Chunk c + 4 of a row
-// (c & 4 == 0) is at the byte offset of chunk c XOR 64, chunk c + 8 at + 2048.
-__device__ __forceinline__ int row_sw(int r) { return ((2 * (r & 3)) | ((r >> 2) & 1)) ^ (2 * ((r >> 3) & 1)); }
+// of 8 rows, row r at 128 (r & 7), its chunk c at slot (c ^ r) & 7 of the segment.  DMA instruction
+// b fills block b (lane l -> slot l), so quarter-wave qq fetches rows 2 qq, 2 qq + 1 as two whole
+// 128-byte segments: whole cache lines per request (a layout that splits each line over two
+// instructions streams ~20% slower per CU).  The XOR by the row was chosen by measurement on gfx950
+// (LDS read probes with the bank-conflict counters): Q.K^T's 16-row operand reads run at the rate of
+// linear ds_read_b128 (192 vs 196 B/clk per CU; a permuted-row swizzle that is conflict-free in a
+// plain 64-bank model reached 128) and the P.V transpose reads at 128 B/clk (linear: 141).  Chunk
+// c + 4 of a row (c & 4 == 0) is at the byte offset of chunk c XOR 64, chunk c + 8 at + 2048.
+__device__ __forceinline__ int row_sw(int r) { return r & 7; }
 __device__ __forceinline__ int slot_byte(int r, int c) {
-    return 1024 * (2 * (c >> 3) + (r >> 3)) + 256 * ((r & 7) >> 1) + 128 * (r & 1) + 16 * ((c & 7) ^ row_sw(r));
+    return 1024 * (2 * (c >> 3) + (r >> 3)) + 128 * (r & 7) + 16 * ((c & 7) ^ row_sw(r));
 }
 
 // Where the V^T / V operand of P.V comes from: two transpose reads per 32-column tile, in 16-lane
