@@ -22,6 +22,10 @@ constexpr int NTHR = 64 * NWAVE;
 constexpr int WK = TK / NWAVE;  // keys per wave slice
 constexpr int HG = 32;          // heads per workgroup
 constexpr float LAZY = 8.0f;    // log2 slack before a reference max moves
+// The lazily moved reference max of a head with no live key yet: below every finite score, so a
+// live key always moves it and exp2(s - M_NONE) of a masked key (s = -inf) is 0 without a special
+// case; a head still at M_NONE after the split had no live key (recorded as -inf).
+constexpr float M_NONE = -3.402823466e38f;      // -FLT_MAX
 constexpr half2 ONE2 = {1.0f16, 1.0f16};
 
 template <int DK>
@@ -269,6 +273,26 @@ __device__ __forceinline__ void stage_q(const DecodeArgs & a, const SliceStream<
     __syncthreads();                         // the q staging in stage 1 is free again
 }
 
+// acc += a . b (v_mfma_f32_16x16x32_f16; first: acc = a . b).  VACC keeps acc in VGPRs through
+// inline asm: in the kernels whose output accumulators fill all 256 AGPRs the compiler selects the
+// AGPR form for every MFMA and would move an output tile out to VGPRs and back around each Q.K^T
+// (48 v_accvgpr moves per slice).  Inline asm is outside the compiler's hazard tracking, so the
+// caller covers the MFMA -> VALU read distance (vacc_settle) before it reads the result.
+template <bool VACC>
+__device__ __forceinline__ void mfma16(f32x4 & acc, const half8 & a, const half8 & b, bool first) {
+    if constexpr (VACC) {
+        if (first) asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+    } else {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, first ? f32x4{0.f, 0.f, 0.f, 0.f} : acc, 0, 0, 0);
+    }
+}
+// 24 wait states after the last MFMA writing acc0..acc3, ahead of any VALU read of them (the
+// operands tie the reads to this point)
+__device__ __forceinline__ void vacc_settle(f32x4 & acc0, f32x4 & acc1, f32x4 & acc2, f32x4 & acc3) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc0), "+v"(acc1), "+v"(acc2), "+v"(acc3));
+}
+
 // S^T = K . Q^T for the wave's 16 keys of the slice at sb (C rows = keys 4 g + r, C cols = heads
 // j16 (acc0) and 16 + j16 (acc1)).  DMA accounting (instructions complete in issue order): the
 // slice is DMA_N blocks then the mask, step s reading blocks 2 (s >> 1) and 2 (s >> 1) + 1; before
@@ -279,16 +303,16 @@ __device__ __forceinline__ void stage_q(const DecodeArgs & a, const SliceStream<
 // use.  Two accumulator chains per head tile (even / odd steps) keep consecutive MFMAs
 // independent.  Returns with the slice's mask slot landed.  WAIT = false: the slice is known to
 // be in LDS already (no DMA accounting, no next-slice DMA).  NT: the cache policy of the next
-// slice's DMA (streaming for decode; cached where other workgroups re-read the cache).
-template <int DK, bool DMA, bool WAIT = true, bool NT = true>
+// slice's DMA (streaming for decode; cached where other workgroups re-read the cache).  VACC: the
+// accumulators in VGPRs (mfma16).
+template <int DK, bool DMA, bool WAIT = true, bool NT = true, bool VACC = false>
 __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const SliceDma & dn, const char * sb, int lane,
                                          const half8 (&qreg)[2][SliceGeom<DK>::QSTEPS], f32x4 & s0, f32x4 & s1) {
     static_assert(WAIT || !DMA, "a slice already in LDS comes with no DMA to spread");
     using G = SliceGeom<DK>;
     constexpr int QPF = 4;
     const int g = lane >> 4, j16 = lane & 15;
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    f32x4 acc2 = {0.f, 0.f, 0.f, 0.f}, acc3 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc0, acc1, acc2, acc3;
     static_assert(QPF % 2 == 0, "operand reads ahead by whole block pairs");
     // row j16, chunk 4 s + g: step s at (a0 ^ 64 (s & 1)) + 2048 (s >> 1)
     const int a0 = slot_byte(j16, g);
@@ -308,11 +332,11 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
             abuf[s % QPF] = *arow(s + QPF);
         }
         if (s & 1) {
-            acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc2, 0, 0, 0);
-            acc3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc3, 0, 0, 0);
+            mfma16<VACC>(acc2, av, qreg[0][s], s == 1);
+            mfma16<VACC>(acc3, av, qreg[1][s], s == 1);
         } else {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[0][s], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qreg[1][s], acc1, 0, 0, 0);
+            mfma16<VACC>(acc0, av, qreg[0][s], s == 0);
+            mfma16<VACC>(acc1, av, qreg[1][s], s == 0);
         }
         if constexpr (DMA) ss.template put<NT>(dn, s);
         __builtin_amdgcn_sched_barrier(0);
@@ -323,36 +347,48 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
     } else if constexpr (WAIT) {
         wait_vm<0>();
     }
+    if constexpr (VACC) vacc_settle(acc0, acc1, acc2, acc3);
     s0 = acc0 + acc2;
     s1 = acc1 + acc3;
 }
 
-// Scores in log2 units of keys kbase + 4 g + r for heads j16 (sc[0]) and 16 + j16 (sc[1]); masked,
-// padded and out-of-range keys are -inf.  mk = the mask values of those 4 keys (zeros without a
-// mask).  mx = the slice's max per head over its 16 keys.
 // the mask values of keys 4 g .. 4 g + 3 of the slice at sb (its mask slot)
 template <int DK>
 __device__ __forceinline__ f32x4 slice_mask(const char * sb, int lane) {
     return *reinterpret_cast<const f32x4 *>(sb + SliceGeom<DK>::ROWS_BYTES + 16 * (lane >> 4));
 }
 
+// Scores in log2 units of keys kbase + 4 g + r for heads j16 (sc[0]) and 16 + j16 (sc[1]); masked,
+// padded and out-of-range keys are -inf.  mk = the mask values of those 4 keys (zeros without a
+// mask).  mx = the slice's max per head over its 16 keys (ACROSS), or over this lane's 4 keys.
+template <bool ACROSS = true>
 __device__ __forceinline__ void slice_scores(const DecodeArgs & a, const f32x4 & mk, int kbase, int lane, const f32x4 & s0,
                                              const f32x4 & s1, float (&sc)[2][4], float (&mx)[2]) {
     const int g = lane >> 4;
     mx[0] = -INFINITY;
     mx[1] = -INFINITY;
+    const int kq = kbase + 4 * g;                    // this lane's first key
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const bool live = kbase + 4 * g + r < a.n_kv;
-        const float mb = mk[r] * LOG2E;              // zeros when there is no mask
-        sc[0][r] = live ? s0[r] * a.scale_log2 + mb : -INFINITY;
-        sc[1][r] = live ? s1[r] * a.scale_log2 + mb : -INFINITY;
+        // a key past n_kv (its K row reads as zeros, so its raw score is 0) takes a -inf mask
+        const float mb = (kq + r < a.n_kv) ? mk[r] * LOG2E : -INFINITY;     // mk: zeros without a mask
+        sc[0][r] = s0[r] * a.scale_log2 + mb;
+        sc[1][r] = s1[r] * a.scale_log2 + mb;
         mx[0] = fmaxf(mx[0], sc[0][r]);
         mx[1] = fmaxf(mx[1], sc[1][r]);
     }
+    if constexpr (ACROSS) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n) mx[n] = rows4_max(mx[n]);
+        for (int n = 0; n < 2; ++n) mx[n] = rows4_max(mx[n]);
+    }
 }
+
+// Whether a head's lazily moved reference max m (M_NONE before its first live key) must move for
+// scores whose max is x: x exceeds m by more than 2^LAZY (any live key, while m = M_NONE).  A
+// head's slice max exceeds the bound iff one of its four lanes' own maxima does, so the kernels
+// test the lanes' own maxima first and take the cross-lane max only on the (rare) path where some
+// reference moves.
+__device__ __forceinline__ bool ref_moves(float m, float x) { return x > m + LAZY; }
 
 }  // namespace decode
 }  // namespace mla

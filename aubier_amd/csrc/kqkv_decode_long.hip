@@ -67,7 +67,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
     stage_q<DK>(a, ss, ring, hg0, t, lane, qreg);
 
     // ---- per-wave state: reference max, l from the f16 P operands, o^T over all columns ----
-    float m_run[2] = {-INFINITY, -INFINITY}; // heads 16 n + j16, log2 units
+    float m_run[2] = {M_NONE, M_NONE};       // heads 16 n + j16, log2 units
     // sum of the P values this lane feeds to the P.V MFMAs: head lane & 31, keys 8 (lane >> 5) .. +7
     // of each of the wave's slices (lane ^ 32 holds the other half)
     float l_acc = 0.0f;
@@ -87,18 +87,19 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
         const char * sb = ring + ss.stage_off(k & 1, w);
         const int kbase = (ss.t0 + k) * TK + WK * w;
         f32x4 s0, s1;
-        if (k + 1 < n_my) qk_slice<DK, true>(ss, dn, sb, lane, qreg, s0, s1);
-        else qk_slice<DK, false>(ss, dn, sb, lane, qreg, s0, s1);
+        if (k + 1 < n_my) qk_slice<DK, true, true, true, true>(ss, dn, sb, lane, qreg, s0, s1);
+        else qk_slice<DK, false, true, true, true>(ss, dn, sb, lane, qreg, s0, s1);
         float sc[2][4], mx[2];
-        slice_scores(a, slice_mask<DK>(sb, lane), kbase, lane, s0, s1, sc, mx);
-        bool mv[2];
-#pragma unroll
-        for (int n = 0; n < 2; ++n) mv[n] = (m_run[n] == -INFINITY) ? (mx[n] != -INFINITY) : (mx[n] > m_run[n] + LAZY);
-        if (__builtin_amdgcn_ballot_w64(mv[0] || mv[1]) != 0) {     // rare: move the reference, rescale
+        slice_scores<false>(a, slice_mask<DK>(sb, lane), kbase, lane, s0, s1, sc, mx);     // this lane's maxima
+        if (__builtin_amdgcn_ballot_w64(ref_moves(m_run[0], mx[0]) || ref_moves(m_run[1], mx[1])) != 0) {
+            // rare: move the reference to the head's slice max, rescale
             float al[2];
+            bool mv[2];
 #pragma unroll
             for (int n = 0; n < 2; ++n) {
-                al[n] = !mv[n] ? 1.0f : (m_run[n] == -INFINITY ? 0.0f : exp2_fast(m_run[n] - mx[n]));
+                mx[n] = rows4_max(mx[n]);
+                mv[n] = ref_moves(m_run[n], mx[n]);
+                al[n] = !mv[n] ? 1.0f : exp2_fast(m_run[n] - mx[n]);     // 0 from M_NONE
                 m_run[n] = mv[n] ? mx[n] : m_run[n];
             }
             const float a_own = al[own_h];
@@ -124,10 +125,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
         uint32_t px[2], py[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const float x0 = exp2_unless(sc[0][2 * e] == -INFINITY, sc[0][2 * e] - m_run[0]);
-            const float x1 = exp2_unless(sc[0][2 * e + 1] == -INFINITY, sc[0][2 * e + 1] - m_run[0]);
-            const float y0 = exp2_unless(sc[1][2 * e] == -INFINITY, sc[1][2 * e] - m_run[1]);
-            const float y1 = exp2_unless(sc[1][2 * e + 1] == -INFINITY, sc[1][2 * e + 1] - m_run[1]);
+            const float x0 = exp2_fast(sc[0][2 * e] - m_run[0]);
+            const float x1 = exp2_fast(sc[0][2 * e + 1] - m_run[0]);
+            const float y0 = exp2_fast(sc[1][2 * e] - m_run[1]);
+            const float y1 = exp2_fast(sc[1][2 * e + 1] - m_run[1]);
             px[e] = __builtin_bit_cast(uint32_t, half2{to_half(x0), to_half(x1)});
             py[e] = __builtin_bit_cast(uint32_t, half2{to_half(y0), to_half(y1)});
             const auto sw = __builtin_amdgcn_permlane16_swap(px[e], py[e], false, false);
@@ -155,6 +156,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
         }
     }
     wait_vm<0>();                            // nothing of this wave may still target the ring
+#pragma unroll
+    for (int n = 0; n < 2; ++n) m_run[n] = (m_run[n] == M_NONE) ? -INFINITY : m_run[n];     // no live key: -inf
 
     // thread indices re-derived through an opaque move, so that the epilogue's address arithmetic
     // is computed here rather than before the loop and kept alive (or spilled) across it

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
     }
 
     // ---- per-wave state (as in kqkv_decode_long.hip) ----
-    float m_run[2] = {-INFINITY, -INFINITY}; // heads 16 n + j16, log2 units
+    float m_run[2] = {M_NONE, M_NONE};       // heads 16 n + j16, log2 units
     float l_acc = 0.0f;                      // head lane & 31, keys 8 (lane >> 5) .. +7 of each slice
     f32x16 o[C::NB];                         // o^T tile i: C row = column 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3), C col = head lane & 31
 #pragma unroll
@@ -145,20 +145,28 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
 #pragma unroll 1
         for (int ks = 0; ks < NWAVE; ++ks) {
             const char * sb = ring + ss.stage_off(par, ks);
-            f32x4 s0, s1;
-            if (ks == 0 && pf) qk_slice<DK, true, true, false>(ss, dn, sb, lane, qreg, s0, s1);
-            else qk_slice<DK, false, false>(ss, none, sb, lane, qreg, s0, s1);
+            // the slice's mask values, read ahead of Q.K^T so that the scores do not wait on LDS
             const f32x4 mk = *reinterpret_cast<const f32x4 *>(mkb + 64 * ks + 16 * g);
-            float sc[2][4], mx[2];
-            slice_scores(a, mk, key_t + WK * ks, lane, s0, s1, sc, mx);
-            bool mv[2];
+            f32x4 s0, s1;
+            if (ks == 0 && pf) qk_slice<DK, true, true, false, true>(ss, dn, sb, lane, qreg, s0, s1);
+            else qk_slice<DK, false, false, true, true>(ss, none, sb, lane, qreg, s0, s1);
+            // the first V^T operands of P.V, read ahead so that their latency passes under the softmax
+            constexpr int VPF = 3;
+            half8 vb[VPF];
 #pragma unroll
-            for (int n = 0; n < 2; ++n) mv[n] = (m_run[n] == -INFINITY) ? (mx[n] != -INFINITY) : (mx[n] > m_run[n] + LAZY);
-            if (__builtin_amdgcn_ballot_w64(mv[0] || mv[1]) != 0) {     // rare: move the reference, rescale
+            for (int i = 0; i < VPF; ++i) vb[i] = pv.load(sb, i);
+            __builtin_amdgcn_sched_barrier(0);
+            float sc[2][4], mx[2];
+            slice_scores<false>(a, mk, key_t + WK * ks, lane, s0, s1, sc, mx);     // this lane's maxima
+            if (__builtin_amdgcn_ballot_w64(ref_moves(m_run[0], mx[0]) || ref_moves(m_run[1], mx[1])) != 0) {
+                // rare: move the reference to the head's slice max, rescale
                 float al[2];
+                bool mv[2];
 #pragma unroll
                 for (int n = 0; n < 2; ++n) {
-                    al[n] = !mv[n] ? 1.0f : (m_run[n] == -INFINITY ? 0.0f : exp2_fast(m_run[n] - mx[n]));
+                    mx[n] = rows4_max(mx[n]);
+                    mv[n] = ref_moves(m_run[n], mx[n]);
+                    al[n] = !mv[n] ? 1.0f : exp2_fast(m_run[n] - mx[n]);     // 0 from M_NONE
                     m_run[n] = mv[n] ? mx[n] : m_run[n];
                 }
                 const float a_own = al[own_h];
@@ -180,10 +188,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
             uint32_t px[2], py[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const float x0 = exp2_unless(sc[0][2 * e] == -INFINITY, sc[0][2 * e] - m_run[0]);
-                const float x1 = exp2_unless(sc[0][2 * e + 1] == -INFINITY, sc[0][2 * e + 1] - m_run[0]);
-                const float y0 = exp2_unless(sc[1][2 * e] == -INFINITY, sc[1][2 * e] - m_run[1]);
-                const float y1 = exp2_unless(sc[1][2 * e + 1] == -INFINITY, sc[1][2 * e + 1] - m_run[1]);
+                const float x0 = exp2_fast(sc[0][2 * e] - m_run[0]);
+                const float x1 = exp2_fast(sc[0][2 * e + 1] - m_run[0]);
+                const float y0 = exp2_fast(sc[1][2 * e] - m_run[1]);
+                const float y1 = exp2_fast(sc[1][2 * e + 1] - m_run[1]);
                 px[e] = __builtin_bit_cast(uint32_t, half2{to_half(x0), to_half(x1)});
                 py[e] = __builtin_bit_cast(uint32_t, half2{to_half(y0), to_half(y1)});
                 const auto sw = __builtin_amdgcn_permlane16_swap(px[e], py[e], false, false);
@@ -194,10 +202,6 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
 #pragma unroll
             for (int e = 0; e < 8; e += 2) l_acc = __builtin_amdgcn_fdot2(half2{pt[e], pt[e + 1]}, ONE2, l_acc, false);
             {
-                constexpr int VPF = 3;
-                half8 vb[VPF];
-#pragma unroll
-                for (int i = 0; i < VPF; ++i) vb[i] = pv.load(sb, i);
 #pragma unroll
                 for (int i = 0; i < C::NB; ++i) {
                     const half8 va = vb[i % VPF];
@@ -210,6 +214,8 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
     }
     wait_vm<0>();
     __syncthreads();                         // the ring becomes the output staging
+#pragma unroll
+    for (int n = 0; n < 2; ++n) m_run[n] = (m_run[n] == M_NONE) ? -INFINITY : m_run[n];     // no live key: -inf
 
     int tid_e;
     asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"(tid));
