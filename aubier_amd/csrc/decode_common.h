@@ -352,6 +352,46 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
     s1 = acc1 + acc3;
 }
 
+// Q.K^T of a slice already in LDS (no DMA accounting; the prefill's tiles land before a barrier),
+// accumulators in VGPRs.  Operand block st of the wave's rows is read QPF_LANDED steps ahead; the
+// first QPF_LANDED come in `abuf` (qk_operands, which the caller may issue early so that their LDS
+// latency passes under other work).  hook(s) runs after step s's MFMAs: the caller's DMA of the
+// next tile, spread over the steps.
+constexpr int QPF_LANDED = 4;
+template <int DK>
+__device__ __forceinline__ void qk_operands(const char * sb, int lane, half8 (&abuf)[QPF_LANDED]) {
+    const int a0 = slot_byte(lane & 15, lane >> 4);
+#pragma unroll
+    for (int st = 0; st < QPF_LANDED; ++st)
+        abuf[st] = *reinterpret_cast<const half8 *>(sb + (a0 ^ (64 * (st & 1))) + 2048 * (st >> 1));
+}
+template <int DK, typename H>
+__device__ __forceinline__ void qk_slice_landed(const char * sb, int lane, const half8 (&qreg)[2][SliceGeom<DK>::QSTEPS],
+                                                half8 (&abuf)[QPF_LANDED], f32x4 & s0, f32x4 & s1, H && hook) {
+    using G = SliceGeom<DK>;
+    constexpr int QPF = QPF_LANDED;
+    const int a0 = slot_byte(lane & 15, lane >> 4);
+    auto arow = [&](int st) { return reinterpret_cast<const half8 *>(sb + (a0 ^ (64 * (st & 1))) + 2048 * (st >> 1)); };
+    f32x4 acc0, acc1, acc2, acc3;
+#pragma unroll
+    for (int s = 0; s < G::QSTEPS; ++s) {
+        const half8 av = abuf[s % QPF];
+        if (s + QPF < G::QSTEPS) abuf[s % QPF] = *arow(s + QPF);
+        if (s & 1) {
+            mfma16<true>(acc2, av, qreg[0][s], s == 1);
+            mfma16<true>(acc3, av, qreg[1][s], s == 1);
+        } else {
+            mfma16<true>(acc0, av, qreg[0][s], s == 0);
+            mfma16<true>(acc1, av, qreg[1][s], s == 0);
+        }
+        hook(s);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    vacc_settle(acc0, acc1, acc2, acc3);
+    s0 = acc0 + acc2;
+    s1 = acc1 + acc3;
+}
+
 // the mask values of keys 4 g .. 4 g + 3 of the slice at sb (its mask slot)
 template <int DK>
 __device__ __forceinline__ f32x4 slice_mask(const char * sb, int lane) {

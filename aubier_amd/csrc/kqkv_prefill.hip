@@ -123,13 +123,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
         for (int r = 0; r < 16; ++r) o[i][r] = 0.0f;
     const PvAddr pv(lane);
     const int own_h = (lane >> 4) & 1;
-    const SliceDma none{};
 
     for (int k = 0; k < n_my; ++k) {
         wait_vm<0>();                        // this wave's slot of tile k (and its mask row) has landed
         __syncthreads();                     // all four have; every wave is done with tile k - 1
-        // tile k + 1's DMA goes out one instruction per Q.K^T step of the first slice (issued in
-        // one block it stalls the wave for ~1,400 cycles)
         const bool pf = k + 1 < n_my;
         const SliceDma dn = plan((k + 1) & 1, k + 1);
         const int par = k & 1;
@@ -142,14 +139,28 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
             }
             continue;
         }
+        // slice 0's first Q.K^T operands and mask values (later slices': during the P.V before)
+        half8 abuf[QPF_LANDED];
+        qk_operands<DK>(ring + ss.stage_off(par, 0), lane, abuf);
+        f32x4 mk_next = *reinterpret_cast<const f32x4 *>(mkb + 16 * g);
 #pragma unroll 1
         for (int ks = 0; ks < NWAVE; ++ks) {
             const char * sb = ring + ss.stage_off(par, ks);
-            // the slice's mask values, read ahead of Q.K^T so that the scores do not wait on LDS
-            const f32x4 mk = *reinterpret_cast<const f32x4 *>(mkb + 64 * ks + 16 * g);
+            const f32x4 mk = mk_next;
             f32x4 s0, s1;
-            if (ks == 0 && pf) qk_slice<DK, true, true, false, true>(ss, dn, sb, lane, qreg, s0, s1);
-            else qk_slice<DK, false, false, true, true>(ss, none, sb, lane, qreg, s0, s1);
+            // tile k + 1's DMA, one instruction per even Q.K^T step of slices 0 and 1 (row blocks
+            // DMA_N / 2 * ks + s / 2) and the mask slot after slice 1's last step: the CU's 76 KB of
+            // DMA per tile, issued within one slice, held the issuing waves ~450 cycles
+            if (pf && ks < 2) {
+                qk_slice_landed<DK>(sb, lane, qreg, abuf, s0, s1, [&](int st) {
+                    constexpr int HALF = G::DMA_N / 2;
+                    static_assert(G::DMA_N % 2 == 0 && G::QSTEPS == G::DMA_N, "two slices of row blocks");
+                    if ((st & 1) == 0) ss.template put<false>(dn, HALF * ks + st / 2);
+                    else if (st == G::QSTEPS - 1 && ks == 1) ss.template put<false>(dn, G::DMA_N);
+                });
+            } else {
+                qk_slice_landed<DK>(sb, lane, qreg, abuf, s0, s1, [](int) {});
+            }
             // the first V^T operands of P.V, read ahead so that their latency passes under the softmax
             constexpr int VPF = 3;
             half8 vb[VPF];
@@ -207,6 +218,10 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
                     const half8 va = vb[i % VPF];
                     if (i + VPF < C::NB) vb[i % VPF] = pv.load(sb, i + VPF);
                     o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pt, o[i], 0, 0, 0);
+                    if (i == C::NB / 2 && ks + 1 < NWAVE) {     // the next slice's operands and mask
+                        qk_operands<DK>(ring + ss.stage_off(par, ks + 1), lane, abuf);
+                        mk_next = *reinterpret_cast<const f32x4 *>(mkb + 64 * (ks + 1) + 16 * g);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
