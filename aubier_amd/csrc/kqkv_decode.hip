@@ -80,7 +80,7 @@ __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds
     stage_q<DK>(a, ss, ring, hg0, t, lane, qreg);
 
     // ---- running state: reference max identical in every wave; l from the f16 P operands ----
-    float m_ref[2] = {-INFINITY, -INFINITY}; // heads 16 n + j16, log2 units
+    float m_ref[2] = {M_NONE, M_NONE};       // heads 16 n + j16, log2 units
     // sum of the P values this lane feeds to the P.V MFMAs: head lane & 31, keys 8 (lane >> 5) .. +7
     // of each 16-key slice (the lane ^ 32 holds the other half)
     float l_acc = 0.0f;
@@ -117,7 +117,7 @@ __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds
                 half4 ph;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    ph[r] = to_half(exp2_unless(sc[n][r] == -INFINITY, fminf(sc[n][r] - m_ref[n], 15.0f)));
+                    ph[r] = to_half(exp2_fast(fminf(sc[n][r] - m_ref[n], 15.0f)));     // masked: 2^-inf = 0
                 *reinterpret_cast<half4 *>(&pxv[(16 * n + j16) * C::PROW + WK * w + 4 * g]) = ph;
             }
         };
@@ -135,14 +135,14 @@ __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds
         for (int n = 0; n < 2; ++n) {
             const f32x4 r4 = *reinterpret_cast<const f32x4 *>(&red[par][16 * n + j16][0]);
             tm[n] = fmaxf(fmaxf(r4[0], r4[1]), fmaxf(r4[2], r4[3]));
-            move |= (m_ref[n] == -INFINITY) ? (tm[n] != -INFINITY) : (tm[n] > m_ref[n] + LAZY);
+            move |= ref_moves(m_ref[n], tm[n]);
         }
         if (__builtin_amdgcn_ballot_w64(move) != 0) {     // rare: move the reference, rescale, redo P
             float al[2];
 #pragma unroll
             for (int n = 0; n < 2; ++n) {
-                const bool mv = (m_ref[n] == -INFINITY) ? (tm[n] != -INFINITY) : (tm[n] > m_ref[n] + LAZY);
-                al[n] = !mv ? 1.0f : (m_ref[n] == -INFINITY ? 0.0f : exp2_fast(m_ref[n] - tm[n]));
+                const bool mv = ref_moves(m_ref[n], tm[n]);
+                al[n] = !mv ? 1.0f : exp2_fast(m_ref[n] - tm[n]);      // 0 from M_NONE
                 m_ref[n] = mv ? tm[n] : m_ref[n];
             }
             l_acc *= al[(lane >> 4) & 1];         // this lane's head is 16 ((lane >> 4) & 1) + j16
@@ -228,7 +228,7 @@ __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds
     if (w == 0 && lane_e < HG) {
         const float mr = m_ref[(lane_e >> 4) & 1];        // lane_e's head 16 ((lane_e >> 4) & 1) + j16
         *reinterpret_cast<f32x2 *>(rec + part_ml_off(a.n_split, lane_e, sp)) =
-            f32x2{(mr == -INFINITY) ? -INFINITY : mr * LN2, L};                   // m in natural-log units
+            f32x2{(mr == M_NONE) ? -INFINITY : mr * LN2, L};                      // m in natural-log units
     }
     // o / l in f16 through this wave's own slot of the stage the last tile did not use (no wave
     // reads it any more: the last tile's loop-top barrier follows every P.V of the one before),
