@@ -135,6 +135,40 @@ def test_prefill_kernel_causal(dev, dk, dv, n_kv, nt, splits, q_scale):
               3e-3 if q_scale < 1 else 1e-2)
 
 
+@pytest.mark.parametrize("dk,dv,n_kv,nt,S", [
+    (576, 512, 8192, 1, 64),      # barrier-per-tile kernel (2 tiles per split): splits 0-31 fully masked
+    (576, 512, 8192, 1, 8),       # independent-wave kernel (16 tiles per split): splits 0-3
+    (576, 512, 4096, 3, 16),      # batch-of-N rows on the barrier-per-tile kernel
+    (576, 512, 4096, 20, 4),      # prefill kernel (nt >= 16): splits 0-1
+    (320, 256, 4096, 1, 32),
+])
+def test_fully_masked_splits(dev, dk, dv, n_kv, nt, S):
+    """Splits whose every key is masked for a token record (m, l) = (-inf, 0) -- the merge's
+    "empty split", whose o block it never reads -- and splits with live keys a finite m; merged,
+    the output equals the oracle's over the live keys."""
+    kc = I.randn(7400, n_kv * dk).astype(np.float16).reshape(n_kv, dk)
+    q = I.randn(7401, nt * 32 * dk, 0.05).reshape(nt, 32, dk)
+    mask = np.zeros((nt, n_kv), dtype=np.float32)
+    mask[:, : n_kv // 2] = -np.inf           # the first half of the cache hidden from every token
+    mask[:, n_kv // 2 + 7::53] = -np.inf     # and scattered holes in the rest
+    scale = float(np.float32(1.0 / np.sqrt(192.0)))
+    ref = orc.kqkv(kc, q, mask, scale, d_v=dv)
+    kc_d, q_d, m_d = (torch.from_numpy(x).to(dev) for x in (kc, q, mask))
+    part = A.ggml_m4_kqkv_partial(kc_d, q_d, m_d, scale, S, d_v=dv)
+    torch.cuda.synchronize()
+    m, l, _ = A.ops.decode_partials(part, 32, dv)
+    b = orc.split_bounds(n_kv, S)
+    dead = [s_ for s_ in range(S) if b[s_ + 1] <= n_kv // 2]
+    live = [s_ for s_ in range(S) if b[s_] >= n_kv // 2]
+    say(f"{dk}/{dv} n_kv={n_kv} nt={nt} S={S}: {len(dead)} fully masked splits, {len(live)} live")
+    assert dead and live
+    assert np.all(m[:, :, dead] == -np.inf) and np.all(l[:, :, dead] == 0.0)
+    assert np.all(np.isfinite(m[:, :, live])) and np.all(l[:, :, live] > 0.0)
+    out = A.ggml_m4_phase_merge(part, n_head=32, d_v=dv)
+    torch.cuda.synchronize()
+    check(f"fully masked splits {dk}/{dv} nt={nt} S={S} vs oracle", out.cpu().numpy(), ref, 1e-2, 3e-3)
+
+
 @pytest.mark.parametrize("d_n,d_v", [(128, 512), (64, 256)])
 @pytest.mark.parametrize("nt", [1, 5, 16, 37, 130])
 def test_wkb_token_counts(dev, d_n, d_v, nt):
