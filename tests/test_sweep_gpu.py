@@ -1,0 +1,106 @@
+"""Seeded sweep of GGML_OP_M4_KQKV shapes through the C ABI against the CPU oracle.
+
+Every case draws, from a fixed seed: the cache type (f16 / f32) and geometry (the two MFMA
+instantiations, BASELINE's 576/512 and the reference's 320/256, plus one outside them that takes
+the VALU kernel), n_kv (from 1 key to a few thousand, ragged against the 16-key slices and 64-key
+tiles), the token count (decode, batch-of-N rows, prefill), the head count (also partial 32-head
+groups), padded row strides of the cache, q and mask (ggml views), the mask pattern (none,
+scattered holes, causal, per-row regions with empty rows of a split), the q scale (flat or sharp
+softmax) and the split count (the library's own, or an explicit one through the partial + merge
+ops).  Tolerances as test_kqkv_gpu.py: f16 cache 1e-2 absolute / 3e-3 relative to max|oracle|
+(2e-2 with a sharp softmax), f32 cache 1e-3 / 1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+import aubier_amd as A
+from aubier_amd import inputs as I
+from oracle import oracle as orc
+
+from conftest import errs, say
+
+pytestmark = pytest.mark.gpu
+
+GEOMS = [(576, 512), (320, 256), (192, 128)]
+N_CASES = 40
+
+
+def draw(i):
+    g = np.random.default_rng(9100 + i)
+    f16 = bool(g.random() < 0.8)
+    dk, dv = GEOMS[g.choice(3, p=[0.6, 0.25, 0.15])]
+    n_kv = int(g.choice([1, 15, 17, 63, 65, 200, 1000, 2049, 4095, 6001]))
+    nt = int(g.choice([1, 1, 2, 3, 7, 16, 17, 20]))
+    H = int(g.choice([32, 32, 1, 7, 33, 48, 64]))
+    mask_kind = str(g.choice(["none", "holes", "causal", "regions"]))
+    q_scale = float(g.choice([0.05, 0.05, 1.0, 30.0]))
+    pad_k = int(g.choice([0, 8, 64]))            # extra elements per cache row (a strided view)
+    pad_q = int(g.choice([0, 4]))                # extra floats per head row of q
+    n_split = None if g.random() < 0.5 else int(g.integers(1, 300))
+    return dict(f16=f16, dk=dk, dv=dv, n_kv=n_kv, nt=nt, H=H, mask_kind=mask_kind, q_scale=q_scale,
+                pad_k=pad_k, pad_q=pad_q, n_split=n_split, seed=9200 + i)
+
+
+def make_mask(c, g):
+    nt, n_kv = c["nt"], c["n_kv"]
+    kind = c["mask_kind"]
+    if kind == "none":
+        return None
+    m = np.zeros((nt, n_kv), dtype=np.float32)
+    if kind == "holes":
+        m[g.random((nt, n_kv)) < 0.2] = -np.inf
+        m[:, 0] = 0.0                              # every row keeps a live key
+    elif kind == "causal":
+        for t in range(nt):
+            m[t, n_kv - nt + t + 1:] = -np.inf
+        m[:, 0] = 0.0
+    else:                                          # per-row regions (batch-of-N sequences)
+        for t in range(nt):
+            a = int(g.integers(0, n_kv))
+            b = int(g.integers(a + 1, n_kv + 1))
+            m[t, :a] = -np.inf
+            m[t, b:] = -np.inf
+    return m
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_kqkv_sweep(dev, i):
+    c = draw(i)
+    g = np.random.default_rng(c["seed"])
+    dk, dv, n_kv, nt, H = c["dk"], c["dv"], c["n_kv"], c["nt"], c["H"]
+    kc = (g.standard_normal((n_kv, dk)) * 0.05).astype(np.float16 if c["f16"] else np.float32)
+    q = (g.standard_normal((nt, H, dk)) * c["q_scale"]).astype(np.float32)
+    mask = make_mask(c, g)
+    scale = float(np.float32(1.0 / np.sqrt(192.0)))
+    ref = orc.kqkv(kc, q, mask, scale, d_v=dv)
+
+    # device tensors as padded ggml views: cache rows, q head rows and mask rows with a stride
+    kc_t = torch.zeros((n_kv, dk + c["pad_k"]), dtype=torch.float16 if c["f16"] else torch.float32)
+    kc_t[:, :dk] = torch.from_numpy(kc)
+    kc_d = kc_t.to(dev)[:, :dk]
+    q_t = torch.zeros((nt, H, dk + c["pad_q"]), dtype=torch.float32)
+    q_t[:, :, :dk] = torch.from_numpy(q)
+    q_d = q_t.to(dev)[:, :, :dk]
+    m_d = None
+    if mask is not None:
+        m_t = torch.zeros((nt, n_kv + 4), dtype=torch.float32)
+        m_t[:, :n_kv] = torch.from_numpy(mask)
+        m_d = m_t.to(dev)[:, :n_kv]
+    say(f"case {i}: {c}")
+    if c["n_split"] is None:
+        out = A.ggml_m4_kqkv(kc_d, q_d, m_d, scale, out=torch.empty((H, nt, dv), dtype=torch.float32, device=dev))
+    else:
+        part = A.ggml_m4_kqkv_partial(kc_d, q_d, m_d, scale, c["n_split"], d_v=dv)
+        out = A.ggml_m4_phase_merge(part, n_head=H, d_v=dv)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ea, er, rr = errs(got, ref)
+    say(f"case {i}: max_abs={ea:.3e} max_rel={er:.3e} rms_rel={rr:.3e}")
+    assert np.isfinite(got).all()
+    if c["f16"]:
+        ta, tr = 1e-2, (2e-2 if c["q_scale"] > 1.0 else 3e-3)
+    else:
+        ta, tr = 1e-3, (1e-4 if c["q_scale"] > 1.0 else 1e-5)
+    assert ea <= ta, (i, ea)
+    assert er <= tr, (i, er)
