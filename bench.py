@@ -274,38 +274,32 @@ def prefill_bench(args, inp) -> int:
         A.ggml_m4_wkb(wkb_w, qd[:, :, :I.D_NOPE], out=qcur[:, :, :DV])
         A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws)
 
-    for _ in range(2):
-        step()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        step()
-    reps = max(3, args.steps // 40)
-    g.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / reps
+    # a graph holds NG back-to-back calls, so that a graph launch's own overhead (~10 us, more than
+    # the smaller kernels here) is spread over them
+    NG = 4
 
-    def time_fn(fn, n=3):
+    def time_fn(fn, reps=3):
         fn()
         torch.cuda.synchronize()
         gg = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gg):
-            fn()
+            for _ in range(NG):
+                fn()
         gg.replay()
         torch.cuda.synchronize()
         a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a0.record()
-        for _ in range(n):
+        for _ in range(reps):
             gg.replay()
         a1.record()
         torch.cuda.synchronize()
-        return a0.elapsed_time(a1) * 1000.0 / n
+        return a0.elapsed_time(a1) * 1000.0 / (reps * NG)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    reps = max(3, args.steps // (4 * NG))
+    us = time_fn(step, reps)
 
     part = None
     n_split = max(1, need // (((H + 31) // 32) * T * A.ops.part_floats(DV) * 4)) if need else 1
@@ -324,7 +318,7 @@ def prefill_bench(args, inp) -> int:
     flop_attn = float((2.0 * H * (DK + DV) * live).sum())
     tf_attn = flop_attn / (us_attn * 1e-6) / 1e12
     rec = {"metric": "MLA chunked prefill (config 5): us/step and TFLOP/s of exact causal work", "value": round(us, 2),
-           "unit": "us/step", "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": round(us / 1000.0, 4),
+           "unit": "us/step", "n_gpus": 1, "steps": reps * NG, "warmup": 3, "ms_per_step": round(us / 1000.0, 4),
            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
            "config": {"workload": f"config 5: {T} tokens x {inp.n_kv} keys causal, 32 heads, f16 cache", "nt": T,
                       "n_kv": inp.n_kv},
