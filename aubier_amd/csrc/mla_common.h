@@ -166,13 +166,8 @@ __device__ __forceinline__ void wait_vm_le(int n) {
         wait_vm_le<N + 1>(n);
     }
 }
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// 16-byte global load/store helpers
-__device__ __forceinline__ u32x4 ld16(const void * p) { return *reinterpret_cast<const u32x4 *>(p); }
-__device__ __forceinline__ u32x4 ld16_stream(const void * p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-}
+// 16-byte streaming (non-temporal) global load
 __device__ __forceinline__ f32x4 ld16f_stream(const void * p) {
     return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
 }
