@@ -12,11 +12,15 @@
 //     LDS ring (decode_common.h layout, cached DMA: the cache is re-read by every token group and
 //     stays in L2 / MALL) plus its own token's 64 mask values, and then every wave runs all four
 //     slices -- 4 tokens x 32 heads share each K / V byte read from LDS.  One workgroup barrier
-//     per tile; the next tile's DMA goes out one instruction per Q.K^T step of the first slice.
-//   * Per slice: S^T = K . Q^T (16 keys x 32 heads, v_mfma_f32_16x16x32_f16), scores with the
-//     token's mask, a lazily moved reference max (P = exp2(s - m) <= 256), P^T for P.V by two
-//     v_permlane16_swap, o^T += V^T . P^T (v_mfma_f32_32x32x16_f16, V^T by ds_read_b64_tr_b16).
-//     l is summed from the same f16 P values.  q and P enter as f16, ggml-cpu's rounding points.
+//     per tile; the next tile's DMA goes out one instruction per even Q.K^T step of the first two
+//     slices.
+//   * Per slice: S^T = K . Q^T (16 keys x 32 heads, v_mfma_f32_16x16x32_f16, accumulators in
+//     VGPRs: the output tiles fill the AGPRs), scores with the token's mask, a lazily moved
+//     reference max (P = exp2(s - m) <= 256; the move test on each lane's own maxima), P^T for P.V
+//     by two v_permlane16_swap, o^T += V^T . P^T (v_mfma_f32_32x32x16_f16, V^T by
+//     ds_read_b64_tr_b16).  l is summed from the same f16 P values.  q and P enter as f16,
+//     ggml-cpu's rounding points.  The next slice's first Q.K^T operands and mask values are read
+//     during P.V, the first V^T operands during the softmax.
 //
 // Grid = (n_split, ceil(H/32), ceil(nt/4)), 256 threads.  Output as the decode kernels: partial
 // blocks [group][token][split] (mla_kernels.h) for the merge, or o/l in f32 to dst with one split.
