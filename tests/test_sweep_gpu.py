@@ -10,6 +10,8 @@ softmax) and the split count (the library's own, or an explicit one through the 
 ops).  Tolerances as test_kqkv_gpu.py: f16 cache 1e-2 absolute / 3e-3 relative to max|oracle|
 (2e-2 with a sharp softmax), f32 cache 1e-3 / 1e-5.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -23,7 +25,7 @@ from conftest import errs, say
 pytestmark = pytest.mark.gpu
 
 GEOMS = [(576, 512), (320, 256), (192, 128)]
-N_CASES = 40
+N_CASES = int(os.environ.get("MLA_SWEEP_CASES", "40"))   # more cases on request
 
 
 def draw(i):
