@@ -1,4 +1,4 @@
-"""Seeded sweep of GGML_OP_M4_KQKV shapes through the C ABI against the CPU oracle.
+"""Seeded sweeps of GGML_OP_M4_KQKV and GGML_OP_M4_WKB shapes through the C ABI against the CPU oracle.
 
 Every case draws, from a fixed seed: the cache type (f16 / f32) and geometry (the two MFMA
 instantiations, BASELINE's 576/512 and the reference's 320/256, plus one outside them that takes
@@ -106,3 +106,52 @@ def test_kqkv_sweep(dev, i):
         ta, tr = 1e-3, (1e-4 if c["q_scale"] > 1.0 else 1e-5)
     assert ea <= ta, (i, ea)
     assert er <= tr, (i, er)
+
+
+def draw_wkb(i):
+    g = np.random.default_rng(9500 + i)
+    q8 = bool(g.random() < 0.4)
+    d_n = int(g.choice([64, 128]))
+    d_v = int(g.choice([16, 48, 256, 512, 528]))
+    H = int(g.choice([1, 7, 32, 32, 48]))
+    nt = int(g.choice([1, 2, 15, 16, 17, 128, 129]))
+    pad_q = int(g.choice([0, 4, 64]))           # floats past d_n per head row (the rope part)
+    pad_o = int(g.choice([0, 4, 8]))            # floats past D_v per output head row
+    return dict(q8=q8, d_n=d_n, d_v=d_v, H=H, nt=nt, pad_q=pad_q, pad_o=pad_o, seed=9600 + i)
+
+
+@pytest.mark.parametrize("i", range(max(1, N_CASES // 2)))
+def test_wkb_sweep(dev, i):
+    """GGML_OP_M4_WKB over seeded shapes: f32 W_kb (the GEMV that holds its rows while up to 15
+    tokens stream, and the 16-token-and-up MFMA GEMM with partial tiles) at the f32 bar, Q8_0 W_kb bit-exact;
+    head counts off 32, q a strided view, the output a strided view whose padding must stay
+    untouched."""
+    c = draw_wkb(i)
+    g = np.random.default_rng(c["seed"])
+    d_n, d_v, H, nt = c["d_n"], c["d_v"], c["H"], c["nt"]
+    q = (g.standard_normal((nt, H, d_n + c["pad_q"])) * 0.05).astype(np.float32)
+    qn = np.ascontiguousarray(q[:, :, :d_n])
+    q_d = torch.from_numpy(q).to(dev)[:, :, :d_n]
+    if c["q8"]:
+        w = orc.q8_0_random(c["seed"] + 1, H * d_v, d_n)
+        ref = orc.wkb_q8(w, d_n, d_v, H, qn)
+        w_d = A.Q8_0(torch.from_numpy(np.ascontiguousarray(w)).reshape(H, d_v, d_n // 32 * 34).to(dev), d_n)
+    else:
+        w = (g.standard_normal((H, d_v, d_n)) * 0.05).astype(np.float32)
+        ref = orc.wkb(w, qn)
+        w_d = torch.from_numpy(w).to(dev)
+    sentinel = 12345.0
+    o_full = torch.full((nt, H, d_v + c["pad_o"]), sentinel, dtype=torch.float32, device=dev)
+    say(f"case {i}: {c}")
+    A.ggml_m4_wkb(w_d, q_d, out=o_full[:, :, :d_v])
+    torch.cuda.synchronize()
+    got_full = o_full.cpu().numpy()
+    got = got_full[:, :, :d_v]
+    assert (got_full[:, :, d_v:] == sentinel).all(), "write past D_v"
+    if c["q8"]:
+        say(f"case {i}: max|diff|={np.abs(got - ref).max():.3e}")
+        assert np.array_equal(np.ascontiguousarray(got).view(np.uint32), ref.view(np.uint32))
+    else:
+        ea, er, rr = errs(got, ref)
+        say(f"case {i}: max_abs={ea:.3e} max_rel={er:.3e}")
+        assert ea <= 1e-3 and er <= 1e-5, (i, ea, er)
