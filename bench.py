@@ -33,7 +33,8 @@ METRIC = "µs/decode-step + achieved HBM GB/s (% peak) for MLA attention at 32K 
 HBM_PEAK_GBPS = 8000.0
 N_ROT = 12
 CAL_BYTES = 256 << 20          # calibration copy size (each way) for the HBM traffic counters
-TRAFFIC_FILE = ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json"
+TRAFFIC_FILES = {3: ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",      # per decode config
+                 4: ROOT / "profiles" / "kqkv_decode_long_cfg4_traffic.json"}
 
 
 def parse():
@@ -225,8 +226,9 @@ def main() -> int:
     # HBM bytes per launch of the partial kernel, from the committed rocprofv3 counter summary
     # (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the calibration copy's factor)
     traffic = None
-    if TRAFFIC_FILE.exists():
-        tr = json.loads(TRAFFIC_FILE.read_text())
+    tf_path = TRAFFIC_FILES.get(args.config)
+    if tf_path is not None and tf_path.exists():
+        tr = json.loads(tf_path.read_text())
         if tr.get("config") == args.config and tr.get("splits") == S:
             traffic = int(tr["traffic_bytes"])
 
