@@ -37,6 +37,16 @@ TRAFFIC_FILES = {3: ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",    
                  4: ROOT / "profiles" / "kqkv_decode_long_cfg4_traffic.json"}
 
 
+def partial_kernel_name(kc_f16: bool, n_kv: int, n_split: int) -> str:
+    """The kernel the library launches for the split-K partial: an f16 cache takes the
+    barrier-per-tile kernel for splits of at most 6 64-key tiles and the independent-wave kernel
+    for longer ones (launch_kqkv_decode_f16); an f32 cache takes the VALU kernel."""
+    if not kc_f16:
+        return "kqkv_generic_kernel<f32 cache>"
+    tiles_per_split = -(-(-(-n_kv // 64)) // n_split)
+    return "kqkv_decode_f16_long_kernel<576,512>" if tiles_per_split > 6 else "kqkv_decode_f16_kernel<576,512>"
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -244,7 +254,7 @@ def main() -> int:
                    "n_kv": W, "n_head": H, "d_k": DK, "d_v": DV, "splits": S, "seeds": inp.seeds, "notes": inp.notes},
         "roofline": {"bound": "hbm", "achieved": round(gbps_attn, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps_attn / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "kqkv_decode_f16_kernel<576,512>", "alg_bytes_per_launch": int(bytes_attn),
+                     "kernel": partial_kernel_name(inp.kc_f16, W, S), "alg_bytes_per_launch": int(bytes_attn),
                      "us_per_launch": round(us_attn, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
