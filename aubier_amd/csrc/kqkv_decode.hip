@@ -7,8 +7,11 @@
 //     exactly once per token (MLA's single latent row serves every head).
 //   * Q.K^T and P.V are dense contractions ([32 x D_k].[D_k x keys] and [32 x keys].[keys x D_v],
 //     60 FLOP per cache byte): they run on v_mfma_f32_16x16x32_f16 / v_mfma_f32_32x32x16_f16 with
-//     f32 accumulation.  q and P enter the MFMA as f16 -- the same rounding points as the unfused
-//     ggml-cpu graph, whose mul_mat converts src1 to F16 for an F16 src0.
+//     f32 accumulation.  q enters the MFMA as f16, where the unfused ggml-cpu graph rounds it (its
+//     mul_mat converts src1 to F16 for an F16 src0).  P enters as f16 as well, but UNNORMALISED
+//     (exp2 of the score minus the lazy reference max below, at most 2^8), whereas ggml-cpu rounds
+//     the normalised softmax output to f16; at long context that is subnormal in f16, so the two
+//     rounding points differ (this kernel is the closer of the two to exact arithmetic).
 //   * Work split of a 64-key tile over the 4 waves (one per SIMD): for Q.K^T wave w owns its slice,
 //     keys 16 w .. 16 w + 15, against all 32 heads (decode_common.h: slice DMA into a two-stage
 //     LDS ring, per-block DMA waits, q fragments in VGPRs); for P.V wave w owns the output columns

@@ -1,23 +1,29 @@
 """MLA decode attention benchmark on one MI355X (BASELINE.json metric: us per decode step plus
 achieved HBM GB/s as a fraction of peak, at 32,768 keys).
 
-    python bench.py [--steps K] [--warmup W] [--config 3] [--splits S] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config 3] [--splits S] [--no-cpu] [--no-others]
 
-One step = the MLA attention of one decode token: GGML_OP_M4_WKB (absorbed q_nope written into
-the Qcur buffer) -> GGML_OP_M4_KQKV pass 1 (split-K partials) -> GGML_OP_M4_PHASE merge, through
-the C ABI, on seeded synthetic inputs (aubier_amd.inputs).  The steps are captured in a hipGraph
-(the way the engine runs them) and replayed; consecutive steps read different copies of the KV
-cache and W_kb (12 copies > the 256 MB MALL), so every step streams from HBM (COLD).
+One step = the MLA attention of one decode token, as the engine's layer graph runs it:
+GGML_OP_M4_WKB (absorbed q_nope written into the Qcur buffer) -> GGML_OP_M4_KQKV (the split-K
+partial kernel, then the PHASE merge kernel), through the C ABI, on seeded synthetic inputs
+(aubier_amd.inputs).  The steps are captured in hipGraphs (the way the engine runs them) and
+replayed; consecutive steps read different copies of the KV cache and W_kb (enough copies that
+a full rotation exceeds 512 MiB, twice the 256 MB MALL), so every step streams from HBM (COLD).
+Exactly K steps are timed (whole rotations plus one graph of the remainder), after exactly W
+untimed warm-up steps.
 
 Prints ONE JSON line.  `roofline` is for the dominant kernel (the split-K partial): algorithmic
 bytes per launch (n_kv * (1152 cache + 4 mask) + Qcur) / its average duration, timed with HIP
 events around a graph of back-to-back launches on the stream they run on.  `cpu_baseline` is the
-CPU oracle (the restated unfused ggml graph) on all host cores, same inputs, median of 5.
+CPU oracle (the restated unfused ggml graph) on the host threads this process may use, same
+inputs, median of 5.  `extra.configs` times every other BASELINE config the same way, with the
+error of one GPU step against the CPU oracle, so one run fills the results table.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -31,7 +37,8 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "µs/decode-step + achieved HBM GB/s (% peak) for MLA attention at 32K keys"
 HBM_PEAK_GBPS = 8000.0
-N_ROT = 12
+MFMA_F16_PEAK_TFLOPS = 2500.0
+COLD_BYTES = 512 << 20         # bytes one rotation of step inputs must exceed (2 x the MALL)
 CAL_BYTES = 256 << 20          # calibration copy size (each way) for the HBM traffic counters
 TRAFFIC_FILES = {3: ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",      # per decode config
                  4: ROOT / "profiles" / "kqkv_decode_long_cfg4_traffic.json"}
@@ -47,6 +54,16 @@ def partial_kernel_name(kc_f16: bool, n_kv: int, n_split: int) -> str:
     return "kqkv_decode_f16_long_kernel<576,512>" if tiles_per_split > 6 else "kqkv_decode_f16_kernel<576,512>"
 
 
+def cpu_threads() -> dict:
+    """Host threads for the CPU baseline: every CPU this process may run on, capped by the
+    OMP_NUM_THREADS share the GPU box sets for one GPU."""
+    visible = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    used = min(visible, share) if share > 0 else visible
+    return {"threads": used, "host_cpus_visible": visible, "omp_num_threads": share or None,
+            "os_cpu_count": os.cpu_count()}
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -56,14 +73,214 @@ def parse():
     ap.add_argument("--splits", type=int, default=0, help="split count (0 = library default)")
     ap.add_argument("--batch", type=int, default=0,
                     help="batch-of-N decode: N rows, each over its own 32768/N-cell region of one window")
-    ap.add_argument("--sweep", action="store_true", help="also time S in {64,128,192,256}")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the S in {64,128,192,256} sweep")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--warm", action="store_true", help="also report WARM (one cache) timings")
+    ap.add_argument("--no-others", action="store_true", help="time the headline config only")
     ap.add_argument("--ops", action="store_true",
                     help="time the reference-geometry quantised ops (Q8_0 WKB, PHASE wv_b, PHASE KV-write) instead")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="no timing: run the calibration copy and a few steps, for rocprofv3 --pmc")
     return ap.parse_args()
+
+
+def errors(out: np.ndarray, ref: np.ndarray) -> dict:
+    """max abs error, and max / RMS error relative to max|ref| (the outputs are ~0.05 / sqrt(L))."""
+    d = np.abs(out.astype(np.float64) - ref.astype(np.float64))
+    scale = float(np.abs(ref).max()) or 1.0
+    return {"max_abs": float(d.max()), "max_rel": float(d.max() / scale),
+            "rms_rel": float(np.sqrt((d ** 2).mean()) / scale)}
+
+
+class Decode:
+    """Device buffers and launch closures of one decode configuration (nt rows, W keys)."""
+
+    def __init__(self, inp, splits: int = 0):
+        import torch
+        import aubier_amd as A
+        from aubier_amd import inputs as I
+        self.A, self.I, self.torch, self.inp = A, I, torch, inp
+        dev = torch.device("cuda:0")
+        H, DV, DK = I.N_HEAD, I.D_V, I.D_K
+        self.H, self.DV, self.DK, self.W = H, DV, DK, inp.n_kv
+        es = 2 if inp.kc_f16 else 4
+        self.es = es
+        self.bytes_attn = inp.n_kv * (DK * es + 4) + inp.nt * H * DK * 4           # cache + mask + Qcur
+        self.bytes_wkb = H * DV * I.D_NOPE * 4 + inp.nt * H * I.D_NOPE * 4 + inp.nt * H * DV * 4
+        self.bytes_out = inp.nt * H * DV * 4
+        self.bytes_step = self.bytes_attn + self.bytes_out + self.bytes_wkb
+        kc_bytes = inp.n_kv * DK * es
+        per_step = kc_bytes + H * DV * I.D_NOPE * 4
+        self.n_rot = max(12, math.ceil(COLD_BYTES / per_step))
+        kc0 = torch.from_numpy(np.ascontiguousarray(inp.kcache)).to(dev)
+        wkb0 = torch.from_numpy(inp.w_kb).to(dev)
+        q = np.concatenate([inp.q_nope, inp.q_pe], axis=2).astype(np.float32)
+        q0 = torch.from_numpy(q).to(dev)
+        self.mask = torch.from_numpy(inp.mask).to(dev)
+        self.kcs = [kc0] + [kc0.clone() for _ in range(self.n_rot - 1)]
+        self.wkbs = [wkb0] + [wkb0.clone() for _ in range(self.n_rot - 1)]
+        self.qs = [q0] + [q0.clone() for _ in range(self.n_rot - 1)]
+        self.qcurs = []
+        for i in range(self.n_rot):
+            qc = torch.zeros((inp.nt, H, DK), dtype=torch.float32, device=dev)
+            qc[:, :, DV:] = self.qs[i][:, :, I.D_NOPE:]
+            self.qcurs.append(qc)
+        self.S = splits or A.default_splits(self.W, H, A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32)
+        self.part = self.new_part(self.S)
+        self.out = torch.empty((H, inp.nt, DV), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+
+    def new_part(self, S):
+        return self.torch.empty(((self.H + 31) // 32, self.inp.nt, S, self.A.ops.part_floats(self.DV, self.inp.kc_f16)),
+                                dtype=self.torch.float32, device="cuda:0")
+
+    def wkb(self, i):
+        self.A.ggml_m4_wkb(self.wkbs[i], self.qs[i][:, :, :self.I.D_NOPE], out=self.qcurs[i][:, :, :self.DV])
+
+    def attn(self, i, part=None, S=None):
+        self.A.ggml_m4_kqkv_partial(self.kcs[i], self.qcurs[i], self.mask, self.inp.kq_scale, S or self.S,
+                                    part=part if part is not None else self.part, d_v=self.DV)
+
+    def merge(self, part=None):
+        self.A.ggml_m4_phase_merge(part if part is not None else self.part, out=self.out, n_head=self.H, d_v=self.DV)
+
+    def step(self, i):
+        """WKB -> KQKV pass 1 -> PHASE merge (what GGML_OP_M4_KQKV launches with its workspace)."""
+        self.wkb(i)
+        self.attn(i)
+        self.merge()
+
+    def capture(self, fn, n, start=0):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(2):            # untimed eager warm-up on the capture stream
+                fn((start + i) % self.n_rot)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn((start + i) % self.n_rot)
+        return g
+
+    def time_graph(self, g, reps, per):
+        """us per unit: replay g `reps` times (each replay = `per` units) between two events."""
+        torch = self.torch
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (reps * per)
+
+    def run_steps(self, k, warmup):
+        """Exactly `warmup` untimed then exactly `k` timed steps (whole rotations replayed as one
+        graph, the remainder as another); returns (us per step, wall seconds of the timed region)."""
+        torch = self.torch
+        g_full = self.capture(self.step, self.n_rot)
+        g_rem = {}
+
+        def replay_n(n):
+            for _ in range(n // self.n_rot):
+                g_full.replay()
+            r = n % self.n_rot
+            if r:
+                if r not in g_rem:
+                    g_rem[r] = self.capture(self.step, r)
+                g_rem[r].replay()
+
+        if k % self.n_rot:
+            g_rem[k % self.n_rot] = self.capture(self.step, k % self.n_rot)
+        if warmup % self.n_rot and warmup % self.n_rot not in g_rem:
+            g_rem[warmup % self.n_rot] = self.capture(self.step, warmup % self.n_rot)
+        torch.cuda.synchronize()
+        replay_n(warmup)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        replay_n(k)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return e0.elapsed_time(e1) * 1000.0 / k, wall
+
+    def per_kernel(self, reps):
+        n = self.n_rot
+        us_wkb = self.time_graph(self.capture(self.wkb, n), reps, n)
+        us_attn = self.time_graph(self.capture(self.attn, n), reps, n)
+        us_merge = self.time_graph(self.capture(lambda i: self.merge(), n), reps, n)
+        return us_wkb, us_attn, us_merge
+
+    def warm_step(self, reps):
+        return self.time_graph(self.capture(lambda i: self.step(0), self.n_rot), reps, self.n_rot)
+
+    def split_sweep(self, reps):
+        res = {}
+        for S in (64, 128, 192, 256):
+            p = self.new_part(S)
+            ua = self.time_graph(self.capture(lambda i, p=p, S=S: self.attn(i, p, S), self.n_rot), reps, self.n_rot)
+            um = self.time_graph(self.capture(lambda i, p=p: self.merge(p), self.n_rot), reps, self.n_rot)
+            res[str(S)] = {"us_partial": round(ua, 3), "us_merge": round(um, 3),
+                           "partial_GBps": round(self.bytes_attn / (ua * 1e3), 1)}
+        return res
+
+    def gpu_output(self):
+        self.step(0)
+        self.torch.cuda.synchronize()
+        return self.out.cpu().numpy()
+
+
+def cpu_run(inp, threads, runs):
+    """The CPU oracle's full step (WKB + unfused kq / softmax / kqv): median seconds of `runs`
+    after one warm-up (runs = 1: a single untimed-warm-up-free run), and the oracle output."""
+    from oracle import oracle as orc
+    if runs > 1:
+        orc.mla_step(inp, threads=threads)
+    ts = []
+    ref = None
+    for _ in range(runs):
+        t = time.perf_counter()
+        _, ref = orc.mla_step(inp, threads=threads)
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts), ref
+
+
+def decode_record(inp, args, steps, warmup, reps, sweep, cpu_runs, cpu_thr):
+    """Time one decode config: the step, each kernel, WARM, optionally the split sweep; the CPU
+    oracle beside it and the error of one GPU step against it."""
+    d = Decode(inp, args.splits)
+    us_step, wall = d.run_steps(steps, warmup)
+    us_wkb, us_attn, us_merge = d.per_kernel(reps)
+    rec = {"n_kv": d.W, "nt": inp.nt, "splits": d.S, "cache": "f16" if inp.kc_f16 else "f32",
+           "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot,
+           "us_step": round(us_step, 3), "us_wkb": round(us_wkb, 3), "us_kqkv_partial": round(us_attn, 3),
+           "us_phase_merge": round(us_merge, 3),
+           "alg_bytes_step": int(d.bytes_step), "alg_bytes_partial": int(d.bytes_attn),
+           "step_GBps": round(d.bytes_step / (us_step * 1e3), 1),
+           "step_frac_of_hbm_peak": round(d.bytes_step / (us_step * 1e3) / HBM_PEAK_GBPS, 4),
+           "partial_GBps": round(d.bytes_attn / (us_attn * 1e3), 1),
+           "partial_frac_of_hbm_peak": round(d.bytes_attn / (us_attn * 1e3) / HBM_PEAK_GBPS, 4),
+           "wkb_GBps": round(d.bytes_wkb / (us_wkb * 1e3), 1),
+           "partial_kernel": partial_kernel_name(inp.kc_f16, d.W, d.S),
+           "partial_bytes_written": int(d.part.numel() * 4), "wall_s_timed": round(wall, 6),
+           "warm_us_step": round(d.warm_step(reps), 3)}
+    if sweep:
+        rec["split_sweep"] = d.split_sweep(reps)
+    out = d.gpu_output()
+    if cpu_runs:
+        t, ref = cpu_run(inp, cpu_thr, cpu_runs)
+        rec["cpu_ms"] = round(t * 1e3, 3)
+        rec["cpu_threads"] = cpu_thr
+        rec["err_vs_oracle"] = errors(out, ref)
+    del d
+    import torch
+    torch.cuda.empty_cache()
+    return rec
 
 
 def main() -> int:
@@ -76,7 +293,6 @@ def main() -> int:
     import aubier_amd as A
     from aubier_amd import inputs as I
 
-    dev = torch.device("cuda:0")
     A.load_library()
     if args.ops:
         return ops_bench(args)
@@ -86,172 +302,81 @@ def main() -> int:
     else:
         inp = I.make_config(args.config)
         if inp.nt > 1:
-            return prefill_bench(args, inp)
-    H, DV, DK = I.N_HEAD, I.D_V, I.D_K
-    W = inp.n_kv
-    es = 2 if inp.kc_f16 else 4
-
-    # ---- device buffers: N_ROT copies of the per-layer data (cache, W_kb, q) ----
-    kc0 = torch.from_numpy(np.ascontiguousarray(inp.kcache)).to(dev)
-    wkb0 = torch.from_numpy(inp.w_kb).to(dev)
-    q = np.zeros((inp.nt, H, I.D_NOPE + I.D_ROPE), dtype=np.float32)
-    q[:, :, :I.D_NOPE] = inp.q_nope
-    q[:, :, I.D_NOPE:] = inp.q_pe
-    q0 = torch.from_numpy(q).to(dev)
-    mask = torch.from_numpy(inp.mask).to(dev)
-    kcs = [kc0] + [kc0.clone() for _ in range(N_ROT - 1)]
-    wkbs = [wkb0] + [wkb0.clone() for _ in range(N_ROT - 1)]
-    qs = [q0] + [q0.clone() for _ in range(N_ROT - 1)]
-    qcurs = []
-    for i in range(N_ROT):
-        qc = torch.zeros((inp.nt, H, DK), dtype=torch.float32, device=dev)
-        qc[:, :, DV:] = qs[i][:, :, I.D_NOPE:]
-        qcurs.append(qc)
-    S = args.splits or A.default_splits(W, H, A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32)
-    part = torch.empty(((H + 31) // 32, inp.nt, S, A.ops.part_floats(DV)), dtype=torch.float32, device=dev)
-    out = torch.empty((H, inp.nt, DV), dtype=torch.float32, device=dev)
-    torch.cuda.synchronize()
-
-    def wkb(i):
-        A.ggml_m4_wkb(wkbs[i], qs[i][:, :, :I.D_NOPE], out=qcurs[i][:, :, :DV])
-
-    def attn(i, part_=None, S_=None):
-        A.ggml_m4_kqkv_partial(kcs[i], qcurs[i], mask, inp.kq_scale, S_ or S, part=part_ if part_ is not None else part)
-
-    def merge(part_=None):
-        A.ggml_m4_phase_merge(part_ if part_ is not None else part, out=out)
-
-    def step(i):
-        wkb(i)
-        attn(i)
-        merge()
-
+            rec = prefill_record(inp, args.steps, args.warmup, cpu=not args.no_cpu, cpu_thr=cpu_threads()["threads"])
+            print(json.dumps(rec), flush=True)
+            return 0
     if args.pmc_pass:
-        # the calibration kernel: a plain device copy of CAL_BYTES each way (torch's copy kernel),
-        # then N_ROT eager steps; rocprofv3 reports FETCH_SIZE / WRITE_SIZE per dispatch of each
-        src = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        for i in range(N_ROT):
-            step(i)
-        torch.cuda.synchronize()
-        print(f"pmc pass done: copy {CAL_BYTES} B x3, {N_ROT} steps of config {args.config}, S={S}", flush=True)
-        return 0
+        return pmc_pass(inp, args)
 
-    def capture(fn, n):
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for i in range(2):            # untimed eager warmup on the capture stream
-                fn(i % N_ROT)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g):
-            for i in range(n):
-                fn(i % N_ROT)
-        return g
-
-    def time_graph(g, reps, per):
-        """us per unit: replay g `reps` times (each replay = `per` units) between two events."""
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1000.0 / (reps * per)
-
-    # ---- the timed region: K steps, graph-captured in blocks of N_ROT ----
-    g_step = capture(step, N_ROT)
-    reps = max(1, args.steps // N_ROT)
-    K = reps * N_ROT
-    for _ in range(max(1, args.warmup // N_ROT)):
-        g_step.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(reps):
-        g_step.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    us_step = e0.elapsed_time(e1) * 1000.0 / K
-
-    # ---- per-kernel durations (graphs of back-to-back launches of one kernel, COLD) ----
-    per_reps = max(4, reps)
-    us_wkb = time_graph(capture(wkb, N_ROT), per_reps, N_ROT)
-    us_attn = time_graph(capture(attn, N_ROT), per_reps, N_ROT)
-    us_merge = time_graph(capture(lambda i: merge(), N_ROT), per_reps, N_ROT)
-
-    bytes_attn = W * (DK * es + 4) + inp.nt * H * DK * 4              # cache + mask + Qcur
-    bytes_wkb = H * DV * I.D_NOPE * 4 + inp.nt * H * I.D_NOPE * 4 + inp.nt * H * DV * 4
-    bytes_step_alg = bytes_attn + inp.nt * H * DV * 4 + bytes_wkb     # + final output
-    gbps_attn = bytes_attn / (us_attn * 1e3)
-    gbps_step = bytes_step_alg / (us_step * 1e3)
-
+    thr = cpu_threads()
+    reps = 8
+    d = Decode(inp, args.splits)
+    us_step, wall = d.run_steps(args.steps, args.warmup)
+    us_wkb, us_attn, us_merge = d.per_kernel(reps)
+    warm = d.warm_step(reps)
+    sweep = None if args.no_sweep else d.split_sweep(reps)
+    out = d.gpu_output()
+    W, S, H = d.W, d.S, d.H
     extra = {
         "us_wkb": round(us_wkb, 3), "us_kqkv_partial": round(us_attn, 3), "us_phase_merge": round(us_merge, 3),
-        "step_GBps": round(gbps_step, 1), "step_frac_of_hbm_peak": round(gbps_step / HBM_PEAK_GBPS, 4),
-        "wkb_GBps": round(bytes_wkb / (us_wkb * 1e3), 1),
-        "partial_bytes": int(part.numel() * 4), "alg_bytes_step": int(bytes_step_alg),
-        "wall_s_timed": round(wall, 3),
+        "step_GBps": round(d.bytes_step / (us_step * 1e3), 1),
+        "step_frac_of_hbm_peak": round(d.bytes_step / (us_step * 1e3) / HBM_PEAK_GBPS, 4),
+        "wkb_GBps": round(d.bytes_wkb / (us_wkb * 1e3), 1),
+        "partial_bytes": int(d.part.numel() * 4), "alg_bytes_step": int(d.bytes_step),
+        "rotating_copies": d.n_rot, "wall_s_timed": round(wall, 6),
+        "warm_us_step": round(warm, 3), "split_sweep": sweep,
     }
-    if args.sweep:
-        sweep = {}
-        for S_ in (64, 128, 192, 256):
-            p_ = torch.empty(((H + 31) // 32, inp.nt, S_, A.ops.part_floats(DV)), dtype=torch.float32, device=dev)
-            ua = time_graph(capture(lambda i, p_=p_, S_=S_: attn(i, p_, S_), N_ROT), per_reps, N_ROT)
-            um = time_graph(capture(lambda i, p_=p_: merge(p_), N_ROT), per_reps, N_ROT)
-            sweep[str(S_)] = {"us_partial": round(ua, 3), "us_merge": round(um, 3),
-                              "partial_GBps": round(bytes_attn / (ua * 1e3), 1)}
-        extra["split_sweep"] = sweep
-    if args.warm:
-        g_w = capture(lambda i: step(0), N_ROT)
-        extra["warm_us_step"] = round(time_graph(g_w, per_reps, N_ROT), 3)
+    bytes_attn = d.bytes_attn
+    del d
+    torch.cuda.empty_cache()
 
-    # ---- CPU baseline: the restated unfused ggml graph on the host cores (rank 0, N=1) ----
+    # ---- CPU baseline: the restated unfused ggml graph on the host threads (rank 0, N=1) ----
     cpu = None
     if not args.no_cpu:
-        from oracle import oracle as orc
-        nthr = min(os.cpu_count() or 1, 16)
-        orc.mla_step(inp, threads=nthr)            # warm-up
-        ts = []
-        for _ in range(5):
-            t = time.perf_counter()
-            orc.mla_step(inp, threads=nthr)
-            ts.append(time.perf_counter() - t)
-        t1 = time.perf_counter()
-        orc.mla_step(inp, threads=1)
-        one = time.perf_counter() - t1
-        cpu = {"value": round(statistics.median(ts) * 1e6, 1), "unit": "us/step", "cores": nthr, "kind": "port",
-               "sample": f"config {args.config} full step (WKB + unfused kq/softmax/kqv), median of 5 after 1 warm-up",
-               "value_1thread": round(one * 1e6, 1)}
+        t, ref = cpu_run(inp, thr["threads"], 5)
+        t1, _ = cpu_run(inp, 1, 1)
+        cpu = {"value": round(t * 1e6, 1), "unit": "us/step", "cores": thr["threads"], "kind": "port",
+               "sample": f"config {args.config} full step (WKB + unfused kq/softmax/kqv) on the same inputs, "
+                         f"median of 5 after 1 warm-up",
+               "value_1thread": round(t1 * 1e6, 1), "host_cpus_visible": thr["host_cpus_visible"],
+               "omp_num_threads": thr["omp_num_threads"]}
+        extra["err_vs_oracle"] = errors(out, ref)
+
+    # ---- every other BASELINE config, timed the same way (fills the results table) ----
+    if not args.no_others and not args.batch:
+        others = {}
+        for cfg in (1, 2, 4, 5):
+            if cfg == args.config:
+                continue
+            ic = I.make_config(cfg)
+            if ic.nt > 1:
+                others[str(cfg)] = prefill_record(ic, 16, 4, cpu=not args.no_cpu, cpu_thr=thr["threads"], nested=True)
+            else:
+                others[str(cfg)] = decode_record(ic, args, steps=48, warmup=12, reps=4, sweep=False,
+                                                 cpu_runs=0 if args.no_cpu else 3, cpu_thr=thr["threads"])
+            del ic
+        extra["configs"] = others
 
     # HBM bytes per launch of the partial kernel, from the committed rocprofv3 counter summary
     # (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the calibration copy's factor)
     traffic = None
     tf_path = TRAFFIC_FILES.get(args.config)
-    if tf_path is not None and tf_path.exists():
+    if tf_path is not None and tf_path.exists() and not args.batch:
         tr = json.loads(tf_path.read_text())
         if tr.get("config") == args.config and tr.get("splits") == S:
             traffic = int(tr["traffic_bytes"])
 
+    gbps_attn = bytes_attn / (us_attn * 1e3)
     rec = {
-        "metric": METRIC, "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": K,
+        "metric": METRIC, "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1000.0, 6), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16" if inp.kc_f16 else "f32", "data": "synthetic",
         "config": {"workload": (f"batch-of-{inp.nt} decode: {inp.nt} rows x 32 heads, each over its own "
                                 f"{W // inp.nt}-cell region of one {W}-cell window, " if args.batch else
                                 f"config {args.config}: MLA decode, 1 token x 32 heads, {W} keys, ") +
                                f"{'f16' if inp.kc_f16 else 'f32'} latent+rope cache [{W},576], W_kb f32 [32,512,128], "
-                               f"split-K S={S} + PHASE merge, COLD ({N_ROT} rotating copies), hipGraph",
-                   "n_kv": W, "n_head": H, "d_k": DK, "d_v": DV, "splits": S, "seeds": inp.seeds, "notes": inp.notes},
+                               f"WKB + split-K S={S} + PHASE merge, COLD ({extra['rotating_copies']} rotating copies), hipGraph",
+                   "n_kv": W, "n_head": H, "d_k": I.D_K, "d_v": I.D_V, "splits": S, "seeds": inp.seeds, "notes": inp.notes},
         "roofline": {"bound": "hbm", "achieved": round(gbps_attn, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps_attn / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": partial_kernel_name(inp.kc_f16, W, S), "alg_bytes_per_launch": int(bytes_attn),
@@ -263,7 +388,24 @@ def main() -> int:
     return 0
 
 
-def prefill_bench(args, inp) -> int:
+def pmc_pass(inp, args) -> int:
+    """The calibration kernel (a plain device copy of CAL_BYTES each way, torch's copy kernel),
+    then one rotation of eager steps; rocprofv3 reports FETCH_SIZE / WRITE_SIZE per dispatch."""
+    import torch
+    d = Decode(inp, args.splits)
+    src = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for i in range(d.n_rot):
+        d.step(i)
+    torch.cuda.synchronize()
+    print(f"pmc pass done: copy {CAL_BYTES} B x3, {d.n_rot} steps of config {args.config}, S={d.S}", flush=True)
+    return 0
+
+
+def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = False) -> dict:
     """Config 5 (chunked prefill, nt > 1): WKB -> KQKV through ggml_m4_kqkv, MFMA-bound, reported
     in TFLOP/s of exact causal work against the f16 dense MFMA peak.  Not the headline metric."""
     import torch
@@ -286,11 +428,10 @@ def prefill_bench(args, inp) -> int:
         A.ggml_m4_wkb(wkb_w, qd[:, :, :I.D_NOPE], out=qcur[:, :, :DV])
         A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws)
 
-    # a graph holds NG back-to-back calls, so that a graph launch's own overhead (~10 us, more than
-    # the smaller kernels here) is spread over them
+    # a graph holds NG back-to-back calls, so that a graph launch's own overhead is spread over them
     NG = 4
 
-    def time_fn(fn, reps=3):
+    def time_fn(fn, reps):
         fn()
         torch.cuda.synchronize()
         gg = torch.cuda.CUDAGraph()
@@ -307,41 +448,57 @@ def prefill_bench(args, inp) -> int:
         torch.cuda.synchronize()
         return a0.elapsed_time(a1) * 1000.0 / (reps * NG)
 
-    for _ in range(2):
+    for _ in range(max(1, warmup)):
         step()
     torch.cuda.synchronize()
-    reps = max(3, args.steps // (4 * NG))
+    reps = max(1, math.ceil(steps / NG))
     us = time_fn(step, reps)
 
     part = None
     n_split = max(1, need // (((H + 31) // 32) * T * A.ops.part_floats(DV) * 4)) if need else 1
     if n_split > 1:
-        part = torch.empty(((H + 31) // 32, T, n_split, A.ops.part_floats(DV)), dtype=torch.float32, device=dev)
-    us_wkb = time_fn(lambda: A.ggml_m4_wkb(wkb_w, qd[:, :, :I.D_NOPE], out=qcur[:, :, :DV]))
+        part = torch.empty(((H + 31) // 32, T, n_split, A.ops.part_floats(DV, inp.kc_f16)), dtype=torch.float32, device=dev)
+    us_wkb = time_fn(lambda: A.ggml_m4_wkb(wkb_w, qd[:, :, :I.D_NOPE], out=qcur[:, :, :DV]), 3)
     if part is not None:
-        us_attn = time_fn(lambda: A.ggml_m4_kqkv_partial(kc, qcur, mask, inp.kq_scale, n_split, part=part))
-        us_merge = time_fn(lambda: A.ggml_m4_phase_merge(part, out=out))
+        us_attn = time_fn(lambda: A.ggml_m4_kqkv_partial(kc, qcur, mask, inp.kq_scale, n_split, part=part), 3)
+        us_merge = time_fn(lambda: A.ggml_m4_phase_merge(part, out=out), 3)
     else:
-        us_attn = time_fn(lambda: A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws))
+        us_attn = time_fn(lambda: A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws), 3)
         us_merge = 0.0
+    step()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
     live = (inp.mask == 0).sum(axis=1).astype(np.float64)          # keys visible to each token
     flop = float((2.0 * H * (DK + DV) * live).sum()) + 2.0 * H * DV * I.D_NOPE * T
     tf = flop / (us * 1e-6) / 1e12
     flop_attn = float((2.0 * H * (DK + DV) * live).sum())
     tf_attn = flop_attn / (us_attn * 1e-6) / 1e12
-    rec = {"metric": "MLA chunked prefill (config 5): us/step and TFLOP/s of exact causal work", "value": round(us, 2),
-           "unit": "us/step", "n_gpus": 1, "steps": reps * NG, "warmup": 3, "ms_per_step": round(us / 1000.0, 4),
-           "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-           "config": {"workload": f"config 5: {T} tokens x {inp.n_kv} keys causal, 32 heads, f16 cache", "nt": T,
-                      "n_kv": inp.n_kv},
-           "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
-                        "frac": round(tf / 2500.0, 4), "traffic": None, "gflop_per_step": round(flop / 1e9, 2),
-                        "attention_kernel": {"us": round(us_attn, 2), "tflops": round(tf_attn, 1),
-                                             "frac": round(tf_attn / 2500.0, 4), "splits": n_split}},
-           "cpu_baseline": None,
-           "extra": {"us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2), "us_phase_merge": round(us_merge, 2)}}
-    print(json.dumps(rec), flush=True)
-    return 0
+    cpu_rec, err = None, None
+    if cpu:
+        t, ref = cpu_run(inp, cpu_thr, 1)
+        cpu_rec = {"value": round(t * 1e6, 1), "unit": "us/step", "cores": cpu_thr, "kind": "port",
+                   "sample": "config 5 full step (WKB + unfused kq/softmax/kqv), one run"}
+        err = errors(got, ref)
+    if nested:
+        return {"n_kv": inp.n_kv, "nt": T, "splits": n_split, "cache": "f16", "steps": reps * NG, "warmup": warmup,
+                "us_step": round(us, 2), "tflops_step": round(tf, 1), "frac_of_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                "us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2), "us_phase_merge": round(us_merge, 2),
+                "attention_tflops": round(tf_attn, 1), "attention_frac_of_mfma_peak": round(tf_attn / MFMA_F16_PEAK_TFLOPS, 4),
+                "gflop_per_step": round(flop / 1e9, 2),
+                "cpu_ms": round(cpu_rec["value"] / 1e3, 3) if cpu_rec else None, "cpu_threads": cpu_thr if cpu_rec else None,
+                "err_vs_oracle": err}
+    return {"metric": "MLA chunked prefill (config 5): us/step and TFLOP/s of exact causal work", "value": round(us, 2),
+            "unit": "us/step", "n_gpus": 1, "steps": reps * NG, "warmup": warmup, "ms_per_step": round(us / 1000.0, 4),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+            "config": {"workload": f"config 5: {T} tokens x {inp.n_kv} keys causal, 32 heads, f16 cache", "nt": T,
+                       "n_kv": inp.n_kv},
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None, "gflop_per_step": round(flop / 1e9, 2),
+                         "attention_kernel": {"us": round(us_attn, 2), "tflops": round(tf_attn, 1),
+                                              "frac": round(tf_attn / MFMA_F16_PEAK_TFLOPS, 4), "splits": n_split}},
+            "cpu_baseline": cpu_rec,
+            "extra": {"us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2), "us_phase_merge": round(us_merge, 2),
+                      "err_vs_oracle": err}}
 
 
 def ops_bench(args) -> int:
@@ -351,7 +508,6 @@ def ops_bench(args) -> int:
     Reference figures (RX 9070, m4-wkb.cu:11-12 and m4-phase.cu:8,31) are printed beside them."""
     import torch
     import aubier_amd as A
-    from aubier_amd import inputs as I
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(9100)
 

@@ -121,8 +121,11 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
  *   dst    F32     ne [D_v, nt, H]   contiguous
  *   kq_scale = op_params[0]
  *   dst[h][t][:] = softmax_j(kq_scale * q[t][h].K[j] + mask[t][j]) . V[j][:]
- * An F16 cache runs on MFMA with q and P rounded to f16 (the rounding points of the unfused
- * ggml-cpu graph, whose mul_mat converts src1 to F16 for an F16 src0); an F32 cache runs in f32.
+ * An F16 cache runs on MFMA with q rounded to f16 where the unfused ggml-cpu graph rounds it (its
+ * mul_mat converts src1 to F16 for an F16 src0) and P rounded to f16 UNNORMALISED (exp2 of the
+ * score minus a running reference max, at most 2^8) -- ggml-cpu rounds the normalised P instead,
+ * which is subnormal in f16 at long context, so results differ from the oracle by more than one
+ * rounding there (and are closer to exact arithmetic); an F32 cache runs in f32.
  * nt == 1 is split-K decode (partial + merge, two launches); nt > 1 is the prefill path.
  * `workspace` (device memory, >= mla_m4_kqkv_workspace_bytes()) holds the split-K partials.
  * ------------------------------------------------------------------------------------------- */

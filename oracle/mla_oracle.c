@@ -640,7 +640,9 @@ void orc_rope_yarn_corr_dims(int n_dims, int n_ctx_orig, float freq_base, float 
  *  4. the row as f16 into kcache row kidx (round to nearest even); dst = kcur (f32).
  * The CUDA math of steps 2-3 (rsqrtf, powf, cosf, sinf, logf) is restated with the C library's
  * f32 functions: the GPU result differs by its own math library's ulps, which grow with pos
- * for the rope (documented in the test tolerances). */
+ * for the rope (documented in the test tolerances).
+ * mutant (tests only): 1 sign slip in the rotation, 2 the wrong cache row, 3 the YaRN correction
+ * dims swapped, 4 the YaRN ramp written as clamp(y) instead of 1 - clamp(y). */
 int orc_kvwrite(const float *cur, int64_t n_embd, const uint8_t *w, int64_t d_lat, int64_t n_rope, const float *nw,
                 uint16_t *kcache, int64_t kc_nb1, int64_t kidx, int32_t pos,
                 float freq_base, float freq_scale, float ext_factor, float attn_factor, float beta_fast,
@@ -693,8 +695,10 @@ int orc_kvwrite(const float *cur, int64_t n_embd, const uint8_t *w, int64_t d_la
         float mscale = attn_factor;
         float theta = freq_scale * theta_extrap;
         if (ext_factor != 0.0f) {
-            const float y = ((float)p - corr[0]) / fmaxf(0.001f, corr[1] - corr[0]);
-            const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, y))) * ext_factor;
+            const float c0 = mutant == 3 ? corr[1] : corr[0], c1 = mutant == 3 ? corr[0] : corr[1];   /* swapped dims */
+            const float y = ((float)p - c0) / fmaxf(0.001f, c1 - c0);
+            const float cl = fminf(1.0f, fmaxf(0.0f, y));
+            const float ramp_mix = (mutant == 4 ? cl : 1.0f - cl) * ext_factor;                   /* ramp sign slip */
             theta = theta * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
             mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
         }

@@ -62,18 +62,28 @@ def test_split_count_invariance(dev, n_split):
 
 
 def test_cfg4_max_context(dev):
+    """262,144 keys (the long-split kernel).  All 32 heads (both 16-head halves of every
+    accumulator set) against the f64 brute force at the f16-cache relative bar, and the measured
+    distance to the oracle printed and bounded: the oracle rounds the normalised probabilities
+    (~1/L) to f16, where they are subnormal, which puts it ~7% (relative to max) from f64 at this
+    length; the kernel rounds unnormalised P and must be far closer to f64 than the oracle is."""
     inp = I.make_config(4)
     say(f"cfg4 n_kv={inp.n_kv} live={inp.n_live} {inp.notes}")
     g = upload(inp, dev)
     qcur, out = run_step(g, inp.kq_scale)
     ref = orc.kqkv(inp.kcache, qcur, inp.mask, inp.kq_scale)
-    _, er_orc, _ = check("cfg4 vs oracle", out, ref, True, rel=1.0)
-    hs = slice(0, 4)   # f64 brute force on 4 heads (same inputs, 1/8 of the work)
-    ref64 = orc.attn_f64(inp.kcache, np.ascontiguousarray(qcur[:, hs]), inp.mask, inp.kq_scale)
-    check("cfg4 vs f64 (heads 0-3)", out[hs], ref64, True, rel=TOL64[True])
-    _, er_o64, _ = errs(ref[hs], ref64)
-    say(f"cfg4 oracle vs f64 (heads 0-3): max_rel={er_o64:.3e}")
-    assert errs(out[hs], ref64)[1] < er_o64
+    ref64 = orc.attn_f64(inp.kcache, qcur, inp.mask, inp.kq_scale)
+    _, er_k64, rr_k64 = check("cfg4 vs f64 (all 32 heads)", out, ref64, True, rel=TOL64[True])
+    for h0 in (0, 16):                       # each 16-head half on its own
+        hs = slice(h0, h0 + 16)
+        check(f"cfg4 vs f64 (heads {h0}-{h0 + 15})", out[hs], ref64[hs], True, rel=TOL64[True])
+    _, er_o64, _ = errs(ref, ref64)
+    ea_ko, er_ko, rr_ko = errs(out, ref)
+    say(f"cfg4 kernel vs oracle: max_abs={ea_ko:.3e} max_rel={er_ko:.3e} rms_rel={rr_ko:.3e}; "
+        f"oracle vs f64: max_rel={er_o64:.3e}; kernel vs f64: max_rel={er_k64:.3e}")
+    assert ea_ko <= TOL[True][0]             # the north-star absolute bar
+    assert er_ko <= 0.10                     # measured 0.07: the oracle's subnormal P rounding
+    assert er_k64 < er_o64 / 10              # the kernel is the closer of the two to exact
 
 
 def test_partials_match_oracle(dev):

@@ -11,6 +11,8 @@ they are pinned by:
   * planted mutants (block mix-up, the other quantisation form, a serial sum for the butterfly, a
     sign slip in the rotation, the wrong cache row) that must fail.
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -203,3 +205,75 @@ def test_kvwrite_rope_textbook(pos):
     assert np.abs(dst[d_lat + 1::2] - r1).max() <= tol
     bad = orc.kvwrite(cur, w, d_lat, n_rope, nw, kc, 1, pos, RP_PLAIN, mutant=1)
     assert np.abs(bad[d_lat + 1::2] - r1).max() > 10 * tol
+
+
+def yarn_corr_dims_f64(n_dims, n_ctx_orig, base, beta_fast, beta_slow):
+    """The YaRN correction range (Peng et al., 2023, reference implementation
+    `_yarn_find_correction_range`): the pair index at which a frequency completes `beta` rotations
+    over the original context, floor / ceil, clamped to [0, n_dims - 1]; computed in float64."""
+    def dim(rot):
+        return n_dims * math.log(n_ctx_orig / (rot * 2.0 * math.pi)) / (2.0 * math.log(base))
+    return max(0.0, math.floor(dim(beta_fast))), min(n_dims - 1.0, math.ceil(dim(beta_slow)))
+
+
+def yarn_theta_f64(pos, p, n_dims, rp):
+    """theta of pair p under YaRN, written from the paper's reference implementation: a linear
+    ramp mask over the pair index between the correction dims, mask = (1 - clamp((p - low) /
+    max(high - low, 0.001), 0, 1)) * ext_factor, and the frequency mixed as
+    interp * (1 - mask) + extrap * mask with interp = freq_scale * extrap."""
+    low, high = yarn_corr_dims_f64(n_dims, rp["n_ctx_orig"], rp["freq_base"], rp["beta_fast"], rp["beta_slow"])
+    extrap = pos * rp["freq_base"] ** (-2.0 * p / n_dims)
+    ramp = min(1.0, max(0.0, (p - low) / max(high - low, 0.001)))
+    mask = (1.0 - ramp) * rp["ext_factor"]
+    return rp["freq_scale"] * extrap * (1.0 - mask) + extrap * mask
+
+
+def yarn_rows(gemv, d_lat, n_rope, pos, rp, pairs):
+    """Expected roped rows (x0, x1) of the given pairs: rotated by the YaRN theta and scaled by the
+    YaRN magnitude attn_factor * (1 + 0.1 ln(1 / freq_scale))."""
+    ms = rp["attn_factor"] * (1.0 + 0.1 * math.log(1.0 / rp["freq_scale"]))
+    x0 = gemv[d_lat + 2 * np.asarray(pairs)].astype(np.float64)
+    x1 = gemv[d_lat + 2 * np.asarray(pairs) + 1].astype(np.float64)
+    th = np.array([yarn_theta_f64(pos, p, n_rope, rp) for p in pairs])
+    return (x0 * np.cos(th) - x1 * np.sin(th)) * ms, (x0 * np.sin(th) + x1 * np.cos(th)) * ms
+
+
+def yarn_max_err(dst, gemv, d_lat, n_rope, pos, rp, pairs):
+    r0, r1 = yarn_rows(gemv, d_lat, n_rope, pos, rp, pairs)
+    idx = d_lat + 2 * np.asarray(pairs)
+    return max(np.abs(dst[idx] - r0).max(), np.abs(dst[idx + 1] - r1).max())
+
+
+@pytest.mark.parametrize("pos", [77, 5000])
+def test_kvwrite_yarn_ramp(pos):
+    """YaRN on (ext_factor 1, freq_scale 1/4) at pos > 0, where theta is not zero.  Closed forms at
+    both ends of the ramp -- pairs p <= low keep the extrapolated theta pos * base^(-2p/n), pairs
+    p >= high take freq_scale times it -- and every interior pair against the ramp of the YaRN
+    reference implementation computed here in float64.  Planted mutants (correction dims swapped;
+    the ramp's 1 - clamp(y) written as clamp(y)) must fail the same checks."""
+    rng = np.random.default_rng(33)
+    n_embd, d_lat, n_rope = 4096, 256, 64
+    rp = RP_YARN
+    w, cur, nw, kc, gemv = kv_inputs(rng, n_embd, d_lat, n_rope, 4)
+    low, high = yarn_corr_dims_f64(n_rope, rp["n_ctx_orig"], rp["freq_base"], rp["beta_fast"], rp["beta_slow"])
+    assert orc.rope_yarn_corr_dims(n_rope, rp["n_ctx_orig"], rp["freq_base"], rp["beta_fast"], rp["beta_slow"]) == (low, high)
+    assert 0 < low < high < n_rope // 2 - 1          # both ramp ends and an interior fall inside the pairs
+    lo_pairs = [p for p in range(n_rope // 2) if p <= low]
+    hi_pairs = [p for p in range(n_rope // 2) if p >= high]
+    mid_pairs = [p for p in range(n_rope // 2) if low < p < high]
+    tol = 1e-6 + 4e-7 * pos * np.abs(gemv[d_lat:]).max()
+    dst = orc.kvwrite(cur, w, d_lat, n_rope, nw, kc, 1, pos, rp)
+    # the closed forms at the ends: theta_extrap / freq_scale * theta_extrap, no ramp involved
+    ms = rp["attn_factor"] * (1.0 + 0.1 * math.log(1.0 / rp["freq_scale"]))
+    for pairs, f in ((lo_pairs, 1.0), (hi_pairs, rp["freq_scale"])):
+        p = np.asarray(pairs)
+        th = f * pos * rp["freq_base"] ** (-2.0 * p / n_rope)
+        x0, x1 = gemv[d_lat + 2 * p], gemv[d_lat + 2 * p + 1]
+        assert np.abs(dst[d_lat + 2 * p] - (x0 * np.cos(th) - x1 * np.sin(th)) * ms).max() <= tol
+        assert np.abs(dst[d_lat + 2 * p + 1] - (x0 * np.sin(th) + x1 * np.cos(th)) * ms).max() <= tol
+    # the interior against the reference implementation's ramp
+    assert yarn_max_err(dst, gemv, d_lat, n_rope, pos, rp, mid_pairs) <= tol
+    # the mutants are caught
+    for mutant in (3, 4):
+        bad = orc.kvwrite(cur, w, d_lat, n_rope, nw, kc.copy(), 1, pos, rp, mutant=mutant)
+        assert yarn_max_err(bad, gemv, d_lat, n_rope, pos, rp, list(range(n_rope // 2))) > 10 * tol, mutant
