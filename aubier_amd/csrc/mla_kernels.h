@@ -66,6 +66,8 @@ bool decode_f16_supported(int dk, int dv);
 
 // Generic VALU path (f32 or f16 cache, any D_k <= 1024, D_v <= D_k): one workgroup per
 // (split, head, token).  round16 applies the f16 rounding of q and P (F16 cache semantics).
+// Its splits are balanced runs of GRAN_KEYS-key granules.
+constexpr int GRAN_KEYS = 16;
 hipError_t launch_kqkv_generic(int dk, int dv, int kc_is_f16, const DecodeArgs & a, hipStream_t stream);
 
 // Split-K merge: partial blocks [group][token][split] (o of o_bytes = 2 or 4) -> dst [dv, nt, H]

@@ -118,7 +118,8 @@ bool use_prefill(const KqkvShape & s) { return use_mfma(s) && s.nt >= mla::PREFI
 int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
 
 int default_splits(const KqkvShape & s) {
-    const int64_t tiles = n_tiles_of(s.n_kv);
+    // the unit a split is made of: 64-key tiles (MFMA kernels), 16-key granules (VALU kernel)
+    const int64_t tiles = use_mfma(s) ? n_tiles_of(s.n_kv) : (s.n_kv + mla::GRAN_KEYS - 1) / mla::GRAN_KEYS;
     int64_t groups;   // workgroups per split
     if (use_prefill(s))
         groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) *
