@@ -38,28 +38,6 @@ namespace {
 
 using namespace decode;
 
-template <int DK, int DV>
-struct ShortCfg {
-    using G = SliceGeom<DK>;
-    static_assert(DV % 128 == 0 && DV <= DK, "geometry");
-    static constexpr int DVQ = DV / NWAVE;              // output columns per wave
-    static constexpr int NTQ = DVQ / 32;                // 32-column output tiles per wave
-    static constexpr int PROW = TK + 8;                 // P exchange row pitch (halves)
-    static constexpr int OPITCH = DVQ * 2 + 16;         // f16 output staging row pitch (bytes)
-    static constexpr int CPR = DVQ / 8;                 // 16-byte output chunks per head row
-    static_assert(HG * OPITCH <= G::ROWS_BYTES, "a wave's output staging fits its slot of a stage");
-    static_assert(CPR % 2 == 0, "whole rounds of 64 chunks");
-    static_assert(NWAVE * NTQ - 1 < 64, "P.V operand offsets fit the DS immediate");
-};
-
-// LDS of the kernel: the slice ring, the P exchange and the slice maxima, by tile parity
-template <int DK, int DV>
-struct ShortLds {
-    __attribute__((aligned(16))) char ring[SliceGeom<DK>::RING];       // [stage][wave] K rows + mask
-    __attribute__((aligned(16))) half_t px[2][HG * ShortCfg<DK, DV>::PROW];
-    __attribute__((aligned(16))) float red[2][HG][NWAVE];              // [head][wave]
-};
-
 // One row (token) t of the split: the whole pass, from the q staging to the partial record.
 template <int DK, int DV>
 __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds<DK, DV> & sh) {
@@ -169,90 +147,11 @@ __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds
             __syncthreads();
         }
 
-        // O^T[own columns, heads] += V^T . P^T over the tile's 64 keys (4 slices x 16): the V
-        // operand (column, 8 keys per lane) and the P rows (head, 8 keys per lane) are the A and B
-        // operands of the 32x32x16 MFMA.  The operands of slice ks + 1 are read while the MFMAs
-        // of slice ks run.
-        {
-            half8 pa[2], vb[2][C::NTQ];
-            auto load = [&](int ks, int b) {
-                pa[b] = *reinterpret_cast<const half8 *>(&pxv[(lane & 31) * C::PROW + WK * ks + 8 * (lane >> 5)]);
-                const char * vs = ring + ss.stage_off(par, ks);
-#pragma unroll
-                for (int i = 0; i < C::NTQ; ++i) vb[b][i] = pv.load(vs, C::NTQ * w + i);
-            };
-            load(0, 0);
-#pragma unroll
-            for (int ks = 0; ks < NWAVE; ++ks) {
-                if (ks + 1 < NWAVE) load(ks + 1, (ks + 1) & 1);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int i = 0; i < C::NTQ; ++i)
-                    o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb[ks & 1][i], pa[ks & 1], o[i], 0, 0, 0);
-                const half8 pp = pa[ks & 1];
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) l_acc = __builtin_amdgcn_fdot2(half2{pp[e], pp[e + 1]}, ONE2, l_acc, false);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+        pv_tile<DK, DV>(ring, pxv, par, w, lane, pv, o, l_acc);
     }
     wait_vm<0>();                            // nothing of this wave may still target the ring
 
-    // thread indices re-derived through an opaque move, so that the epilogue's address arithmetic
-    // is computed here rather than before the loop and kept alive (or spilled) across it
-    int tid_e;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(tid_e) : "v"(tid));
-    const int lane_e = tid_e & 63;
-
-    // ---- per head: l over all keys of the split, relative to the common reference m_ref ----
-    // Every wave summed the whole P exchange for its heads, so each finishes on its own: no
-    // workgroup barrier from here on.  The header is (m_ref, l): m_ref lies within 2^8 below the
-    // split's max, which the merge's algebra does not care about (only m + ln l enters it).
-    const float L = halves_sum(l_acc);         // head lane_e & 31
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const int hl = lane_e & 31, hi4 = 4 * (lane_e >> 5);
-
-    const bool direct = a.dst != nullptr;                 // single split: final f32 output to dst
-    if (direct) {
-        const int h = hg0 + hl;
-        if (h < a.n_head) {
-            float * d = a.dst + ((size_t)h * a.nt + t) * DV + C::DVQ * w + hi4;
-#pragma unroll
-            for (int i = 0; i < C::NTQ; ++i)
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4)
-                    *reinterpret_cast<f32x4 *>(d + 32 * i + 8 * q4) =
-                        f32x4{o[i][4 * q4] * inv, o[i][4 * q4 + 1] * inv, o[i][4 * q4 + 2] * inv, o[i][4 * q4 + 3] * inv};
-        }
-        return;
-    }
-    char * rec = part_record(a.part, blockIdx.y, a.nt, t, a.n_split, DV, 2);
-    char * blk = rec + part_o_off(a.n_split, sp, DV, 2);
-    if (w == 0 && lane_e < HG) {
-        const float mr = m_ref[(lane_e >> 4) & 1];        // lane_e's head 16 ((lane_e >> 4) & 1) + j16
-        *reinterpret_cast<f32x2 *>(rec + part_ml_off(a.n_split, lane_e, sp)) =
-            f32x2{(mr == M_NONE) ? -INFINITY : mr * LN2, L};                      // m in natural-log units
-    }
-    // o / l in f16 through this wave's own slot of the stage the last tile did not use (no wave
-    // reads it any more: the last tile's loop-top barrier follows every P.V of the one before),
-    // as [32 heads][DVQ] rows; then 16-byte chunks out, 4 head rows of 2 * DVQ bytes per
-    // instruction (whole cache lines).  Write and read are the same wave's, in LDS order.
-    char * stg = ring + ss.stage_off(n_my & 1, w);
-#pragma unroll
-    for (int i = 0; i < C::NTQ; ++i)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const half4 hv = {to_half(o[i][4 * q4] * inv), to_half(o[i][4 * q4 + 1] * inv), to_half(o[i][4 * q4 + 2] * inv),
-                              to_half(o[i][4 * q4 + 3] * inv)};
-            *reinterpret_cast<half4 *>(stg + hl * C::OPITCH + (32 * i + 8 * q4 + hi4) * 2) = hv;
-        }
-#pragma unroll
-    for (int it = 0; it < C::CPR / 2; ++it) {
-        const int q = 64 * it + lane_e;
-        const int row = q / C::CPR, ch = q % C::CPR;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + row * C::OPITCH + 16 * ch);
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(blk + ((size_t)row * DV + C::DVQ * w + 8 * ch) * 2));
-    }
+    decode_epilogue<DK, DV>(a, ring, n_my, w, tid, t, hg0, sp, o, l_acc, m_ref);
 }
 
 // ROWS = false: row blockIdx.z (one token, the plain decode step).  ROWS = true: rows blockIdx.z,

@@ -177,11 +177,12 @@ class Decode:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1000.0 / (reps * per)
 
-    def run_steps(self, k, warmup):
+    def run_steps(self, k, warmup, step=None):
         """Exactly `warmup` untimed then exactly `k` timed steps (whole rotations replayed as one
         graph, the remainder as another); returns (us per step, wall seconds of the timed region)."""
         torch = self.torch
-        g_full = self.capture(self.step, self.n_rot)
+        step = step or self.step
+        g_full = self.capture(step, self.n_rot)
         g_rem = {}
 
         def replay_n(n):
@@ -190,13 +191,13 @@ class Decode:
             r = n % self.n_rot
             if r:
                 if r not in g_rem:
-                    g_rem[r] = self.capture(self.step, r)
+                    g_rem[r] = self.capture(step, r)
                 g_rem[r].replay()
 
         if k % self.n_rot:
-            g_rem[k % self.n_rot] = self.capture(self.step, k % self.n_rot)
+            g_rem[k % self.n_rot] = self.capture(step, k % self.n_rot)
         if warmup % self.n_rot and warmup % self.n_rot not in g_rem:
-            g_rem[warmup % self.n_rot] = self.capture(self.step, warmup % self.n_rot)
+            g_rem[warmup % self.n_rot] = self.capture(step, warmup % self.n_rot)
         torch.cuda.synchronize()
         replay_n(warmup)
         torch.cuda.synchronize()
@@ -210,11 +211,11 @@ class Decode:
         return e0.elapsed_time(e1) * 1000.0 / k, wall
 
     def per_kernel(self, reps):
+        """Per-launch us of each kernel: graphs of back-to-back launches (COLD)."""
         n = self.n_rot
-        us_wkb = self.time_graph(self.capture(self.wkb, n), reps, n)
-        us_attn = self.time_graph(self.capture(self.attn, n), reps, n)
-        us_merge = self.time_graph(self.capture(lambda i: self.merge(), n), reps, n)
-        return us_wkb, us_attn, us_merge
+        return {"wkb": self.time_graph(self.capture(self.wkb, n), reps, n),
+                "partial": self.time_graph(self.capture(self.attn, n), reps, n),
+                "merge": self.time_graph(self.capture(lambda i: self.merge(), n), reps, n)}
 
     def warm_step(self, reps):
         return self.time_graph(self.capture(lambda i: self.step(0), self.n_rot), reps, self.n_rot)
@@ -250,27 +251,36 @@ def cpu_run(inp, threads, runs):
     return statistics.median(ts), ref
 
 
-def decode_record(inp, args, steps, warmup, reps, sweep, cpu_runs, cpu_thr):
-    """Time one decode config: the step, each kernel, WARM, optionally the split sweep; the CPU
-    oracle beside it and the error of one GPU step against it."""
-    d = Decode(inp, args.splits)
+def decode_timings(d, steps, warmup, reps, sweep):
+    """Time one decode configuration: exactly `steps` steps after `warmup`, each kernel, WARM,
+    optionally the split sweep, and the dominant kernel's roofline."""
     us_step, wall = d.run_steps(steps, warmup)
-    us_wkb, us_attn, us_merge = d.per_kernel(reps)
-    rec = {"n_kv": d.W, "nt": inp.nt, "splits": d.S, "cache": "f16" if inp.kc_f16 else "f32",
-           "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot,
-           "us_step": round(us_step, 3), "us_wkb": round(us_wkb, 3), "us_kqkv_partial": round(us_attn, 3),
-           "us_phase_merge": round(us_merge, 3),
-           "alg_bytes_step": int(d.bytes_step), "alg_bytes_partial": int(d.bytes_attn),
-           "step_GBps": round(d.bytes_step / (us_step * 1e3), 1),
-           "step_frac_of_hbm_peak": round(d.bytes_step / (us_step * 1e3) / HBM_PEAK_GBPS, 4),
-           "partial_GBps": round(d.bytes_attn / (us_attn * 1e3), 1),
-           "partial_frac_of_hbm_peak": round(d.bytes_attn / (us_attn * 1e3) / HBM_PEAK_GBPS, 4),
-           "wkb_GBps": round(d.bytes_wkb / (us_wkb * 1e3), 1),
-           "partial_kernel": partial_kernel_name(inp.kc_f16, d.W, d.S),
-           "partial_bytes_written": int(d.part.numel() * 4), "wall_s_timed": round(wall, 6),
-           "warm_us_step": round(d.warm_step(reps), 3)}
+    k = d.per_kernel(reps)
+    r = {"n_kv": d.W, "nt": d.inp.nt, "splits": d.S, "cache": "f16" if d.inp.kc_f16 else "f32",
+         "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot,
+         "us_step": round(us_step, 3), "wall_s_timed": round(wall, 6),
+         "us_wkb": round(k["wkb"], 3), "us_kqkv_partial": round(k["partial"], 3), "us_phase_merge": round(k["merge"], 3),
+         "alg_bytes_step": int(d.bytes_step),
+         "step_GBps": round(d.bytes_step / (us_step * 1e3), 1),
+         "step_frac_of_hbm_peak": round(d.bytes_step / (us_step * 1e3) / HBM_PEAK_GBPS, 4),
+         "partial_GBps": round(d.bytes_attn / (k["partial"] * 1e3), 1),
+         "partial_frac_of_hbm_peak": round(d.bytes_attn / (k["partial"] * 1e3) / HBM_PEAK_GBPS, 4),
+         "wkb_GBps": round(d.bytes_wkb / (k["wkb"] * 1e3), 1),
+         "partial_kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S),
+         "partial_bytes_written": int(d.part.numel() * 4),
+         "warm_us_step": round(d.warm_step(reps), 3)}
+    r["roofline"] = {"kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S), "alg_bytes_per_launch": int(d.bytes_attn),
+                     "us_per_launch": k["partial"], "timing": "graph of back-to-back launches"}
     if sweep:
-        rec["split_sweep"] = d.split_sweep(reps)
+        r["split_sweep"] = d.split_sweep(reps)
+    return r
+
+
+def decode_record(inp, args, steps, warmup, reps, sweep, cpu_runs, cpu_thr):
+    """decode_timings of one config, the CPU oracle beside it and the error of one GPU step."""
+    d = Decode(inp, args.splits)
+    rec = decode_timings(d, steps, warmup, reps, sweep)
+    rec.pop("roofline")
     out = d.gpu_output()
     if cpu_runs:
         t, ref = cpu_run(inp, cpu_thr, cpu_runs)
@@ -311,22 +321,12 @@ def main() -> int:
     thr = cpu_threads()
     reps = 8
     d = Decode(inp, args.splits)
-    us_step, wall = d.run_steps(args.steps, args.warmup)
-    us_wkb, us_attn, us_merge = d.per_kernel(reps)
-    warm = d.warm_step(reps)
-    sweep = None if args.no_sweep else d.split_sweep(reps)
+    t = decode_timings(d, args.steps, args.warmup, reps, sweep=not args.no_sweep)
     out = d.gpu_output()
     W, S, H = d.W, d.S, d.H
-    extra = {
-        "us_wkb": round(us_wkb, 3), "us_kqkv_partial": round(us_attn, 3), "us_phase_merge": round(us_merge, 3),
-        "step_GBps": round(d.bytes_step / (us_step * 1e3), 1),
-        "step_frac_of_hbm_peak": round(d.bytes_step / (us_step * 1e3) / HBM_PEAK_GBPS, 4),
-        "wkb_GBps": round(d.bytes_wkb / (us_wkb * 1e3), 1),
-        "partial_bytes": int(d.part.numel() * 4), "alg_bytes_step": int(d.bytes_step),
-        "rotating_copies": d.n_rot, "wall_s_timed": round(wall, 6),
-        "warm_us_step": round(warm, 3), "split_sweep": sweep,
-    }
-    bytes_attn = d.bytes_attn
+    us_step = t["us_step"]
+    roof = t.pop("roofline")
+    extra = {k: v for k, v in t.items() if k not in ("n_kv", "nt", "splits", "cache", "steps", "warmup")}
     del d
     torch.cuda.empty_cache()
 
@@ -363,10 +363,11 @@ def main() -> int:
     tf_path = TRAFFIC_FILES.get(args.config)
     if tf_path is not None and tf_path.exists() and not args.batch:
         tr = json.loads(tf_path.read_text())
-        if tr.get("config") == args.config and tr.get("splits") == S:
+        if tr.get("config") == args.config and tr.get("splits") == S and tr.get("kernel") == roof["kernel"]:
             traffic = int(tr["traffic_bytes"])
 
-    gbps_attn = bytes_attn / (us_attn * 1e3)
+    gbps = roof["alg_bytes_per_launch"] / (roof["us_per_launch"] * 1e3)
+    step_desc = "WKB + split-K partial + PHASE merge"
     rec = {
         "metric": METRIC, "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1000.0, 6), "higher_is_better": False,
@@ -375,12 +376,12 @@ def main() -> int:
                                 f"{W // inp.nt}-cell region of one {W}-cell window, " if args.batch else
                                 f"config {args.config}: MLA decode, 1 token x 32 heads, {W} keys, ") +
                                f"{'f16' if inp.kc_f16 else 'f32'} latent+rope cache [{W},576], W_kb f32 [32,512,128], "
-                               f"WKB + split-K S={S} + PHASE merge, COLD ({extra['rotating_copies']} rotating copies), hipGraph",
+                               f"{step_desc} (S={S}), COLD ({extra['rotating_copies']} rotating copies), hipGraph",
                    "n_kv": W, "n_head": H, "d_k": I.D_K, "d_v": I.D_V, "splits": S, "seeds": inp.seeds, "notes": inp.notes},
-        "roofline": {"bound": "hbm", "achieved": round(gbps_attn, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps_attn / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": partial_kernel_name(inp.kc_f16, W, S), "alg_bytes_per_launch": int(bytes_attn),
-                     "us_per_launch": round(us_attn, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": roof["kernel"], "alg_bytes_per_launch": roof["alg_bytes_per_launch"],
+                     "us_per_launch": round(roof["us_per_launch"], 3), "timing": roof["timing"]},
         "cpu_baseline": cpu,
         "extra": extra,
     }
