@@ -15,6 +15,7 @@ from .ops import (  # noqa: F401
     supports_phase_wvb,
     default_splits,
     ggml_m4_kqkv,
+    ggml_m4_kqkv_noalloc,
     ggml_m4_kqkv_partial,
     ggml_m4_phase_merge,
     ggml_m4_wkb,

@@ -6,6 +6,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "../../include/mla_m4.h"
 #include "mla_kernels.h"
@@ -281,6 +282,45 @@ void rope_yarn_corr_dims(int n_dims, int n_ctx_orig, float freq_base, float beta
     dims[1] = end < (float)(n_dims - 1) ? end : (float)(n_dims - 1);
 }
 
+// ---------------------------------------------------------------- static scratch (no-alloc entry)
+// The split-K partials of mla_m4_kqkv_noalloc: a fixed device array that each GPU the library
+// runs on holds until the process ends.  Host code uses only the address hipGetSymbolAddress
+// returns for the current device (the array's name in host code is a host-side stand-in, not a
+// device address), resolved once per device on that device's first call and kept.
+static __device__ __align__(256) unsigned char scratch[MLA_M4_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void * g_scratch_ptr[MAX_DEVICES] = {};
+
+void * scratch_ptr() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void * p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+// The KQKV launch sequence shared by mla_m4_kqkv and mla_m4_kqkv_noalloc: with one split the
+// attention kernel writes dst; otherwise partials into `part` (>= part_bytes(s, sp)) and the merge.
+int kqkv_launch(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask, float kq_scale,
+                const mla_m4_tensor * dst, const KqkvShape & s, int sp, char * part, hipStream_t st) {
+    mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, sp);
+    if (sp == 1) {
+        a.dst = static_cast<float *>(dst->data);
+        return launch_attn(s, a, st);
+    }
+    a.part = part;
+    const int rc = launch_attn(s, a, st);
+    if (rc != MLA_M4_OK) return rc;
+    return mla::launch_merge(a.part, (int)s.dv, part_o_bytes(s), sp, (int)s.nt, (int)s.n_head, static_cast<float *>(dst->data), st) == hipSuccess
+               ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
 }  // namespace
 
 extern "C" {
@@ -298,6 +338,7 @@ const char * mla_m4_status_str(int status) {
         case MLA_M4_ERR_ARG: return "scalar argument out of range";
         case MLA_M4_ERR_LAUNCH: return "HIP launch failed";
         case MLA_M4_ERR_UNSUPPORTED: return "shape not implemented by these kernels";
+        case MLA_M4_ERR_SCRATCH: return "needs more than the static scratch holds (or its address is unavailable)";
         default: return "unknown status";
     }
 }
@@ -341,22 +382,28 @@ int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type
 int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask, float kq_scale,
                 const mla_m4_tensor * dst, void * workspace, size_t workspace_bytes, void * stream) {
     KqkvShape s{};
-    int rc = check_kqkv(kcache, q, mask, dst, &s);
+    const int rc = check_kqkv(kcache, q, mask, dst, &s);
     if (rc != MLA_M4_OK) return rc;
     if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
     const int sp = (s.dv & 7) ? 1 : default_splits(s);     // the merge reads 8 columns at a time
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, sp);
-    if (sp == 1) {
-        a.dst = static_cast<float *>(dst->data);
-        return launch_attn(s, a, st);
-    }
-    if (!workspace || !aligned16(workspace) || workspace_bytes < part_bytes(s, sp)) return MLA_M4_ERR_WORKSPACE;
-    a.part = static_cast<char *>(workspace);
-    rc = launch_attn(s, a, st);
+    if (sp > 1 && (!workspace || !aligned16(workspace) || workspace_bytes < part_bytes(s, sp))) return MLA_M4_ERR_WORKSPACE;
+    return kqkv_launch(kcache, q, mask, kq_scale, dst, s, sp, static_cast<char *>(workspace), static_cast<hipStream_t>(stream));
+}
+
+int mla_m4_kqkv_noalloc(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask, float kq_scale,
+                        const mla_m4_tensor * dst, void * stream) {
+    KqkvShape s{};
+    const int rc = check_kqkv(kcache, q, mask, dst, &s);
     if (rc != MLA_M4_OK) return rc;
-    return mla::launch_merge(a.part, (int)s.dv, part_o_bytes(s), sp, (int)s.nt, (int)s.n_head, static_cast<float *>(dst->data), st) == hipSuccess
-               ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+    if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
+    const int sp = (s.dv & 7) ? 1 : default_splits(s);
+    char * part = nullptr;
+    if (sp > 1) {
+        if (part_bytes(s, sp) > MLA_M4_NOALLOC_SCRATCH_BYTES) return MLA_M4_ERR_SCRATCH;
+        part = static_cast<char *>(scratch_ptr());
+        if (part == nullptr) return MLA_M4_ERR_SCRATCH;
+    }
+    return kqkv_launch(kcache, q, mask, kq_scale, dst, s, sp, part, static_cast<hipStream_t>(stream));
 }
 
 int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask,

@@ -50,6 +50,7 @@ STATUS = {
     -3: "shape violates the op contract", -4: "strides/alignment violate the op contract",
     -5: "workspace missing or too small", -6: "scalar argument out of range",
     -7: "HIP launch failed", -8: "shape not implemented by these kernels",
+    -9: "needs more than the static scratch holds (or its address is unavailable)",
 }
 
 
@@ -83,6 +84,8 @@ _EXPORTS = {
     "mla_m4_wkb": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_void_p]),
     "mla_m4_kqkv": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_float, ctypes.POINTER(MlaTensor),
                                                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mla_m4_kqkv_noalloc": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_float, ctypes.POINTER(MlaTensor),
+                                                                              ctypes.c_void_p]),
     "mla_m4_kqkv_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(MlaTensor)] * 3),
     "mla_m4_kqkv_default_splits": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
     "mla_m4_kqkv_partial": (ctypes.c_int, [ctypes.POINTER(MlaTensor)] * 3 + [ctypes.c_float, ctypes.c_int, ctypes.c_int64,
@@ -239,6 +242,22 @@ def ggml_m4_kqkv(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[torch.Ten
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check("ggml_m4_kqkv", lib.mla_m4_kqkv(_ptr(vk), _ptr(vq), _ptr(vm), ctypes.c_float(kq_scale), _ptr(vo),
                                            ws_ptr, ws_bytes, _stream(q)))
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+
+def ggml_m4_kqkv_noalloc(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[torch.Tensor], kq_scale: float,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """ggml_m4_kqkv without a workspace: the library's static scratch holds the split-K partials
+    (include/mla_m4.h mla_m4_kqkv_noalloc; calls that overlap on one GPU race)."""
+    lib = load_library()
+    if out is None:
+        dv = 512 if kcache.shape[1] == 576 else (256 if kcache.shape[1] == 320 else kcache.shape[1])
+        out = torch.empty((q.shape[1], q.shape[0], dv), dtype=torch.float32, device=q.device)
+    _check("ggml_m4_kqkv_noalloc", lib.mla_m4_kqkv_noalloc(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(mask)),
+                                                           ctypes.c_float(kq_scale), _ptr(view(out)), _stream(q)))
     return out
 
 

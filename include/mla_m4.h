@@ -47,7 +47,9 @@ enum {
     MLA_M4_ERR_WORKSPACE  = -5,  /* workspace missing or smaller than mla_m4_kqkv_workspace_bytes() */
     MLA_M4_ERR_ARG        = -6,  /* a scalar argument is out of range (split count, phase id, ...) */
     MLA_M4_ERR_LAUNCH     = -7,  /* the HIP launch failed (hipGetLastError) */
-    MLA_M4_ERR_UNSUPPORTED = -8  /* a legal ggml shape these kernels do not implement */
+    MLA_M4_ERR_UNSUPPORTED = -8, /* a legal ggml shape these kernels do not implement */
+    MLA_M4_ERR_SCRATCH    = -9   /* mla_m4_kqkv_noalloc: the partials exceed its static scratch, or
+                                    the scratch address could not be resolved */
 };
 
 /* A device tensor view: the data/type/ne/nb fields of a ggml_tensor (ggml.h struct ggml_tensor). */
@@ -136,6 +138,23 @@ int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
 /* Workspace bytes mla_m4_kqkv needs for these shapes (0 when no partials are used). */
 size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
                                    const mla_m4_tensor * dst);
+
+/* -------------------------------------------------------------------------------------------
+ * mla_m4_kqkv without a workspace argument -- no counterpart in the reference's interface; for
+ * callers that cannot allocate (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same operands, launches and results as mla_m4_kqkv (bit for bit); the
+ * split-K partials live in a static device array of MLA_M4_NOALLOC_SCRATCH_BYTES (32 MiB) that
+ * each GPU the library runs on holds until the process ends.  With an f16 cache a 32-head group
+ * at 256 splits (>= 16K keys) needs 8.45 MB per token, so decode of up to 3 tokens at H <= 32
+ * fits; the f32-cache kernel uses ~256 / (H nt) splits (0.53 MB at H = 32, one token).  Shapes
+ * that need more (prefill, more heads) return MLA_M4_ERR_SCRATCH.  Allocates nothing and calls
+ * no allocating routine; the first call on each device resolves the array's address
+ * (hipGetSymbolAddress), so make that first call outside graph capture.  Every call on a GPU uses that GPU's one array: calls that overlap on one GPU
+ * (concurrent streams) race.
+ * ------------------------------------------------------------------------------------------- */
+#define MLA_M4_NOALLOC_SCRATCH_BYTES (32u << 20)
+int mla_m4_kqkv_noalloc(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
+                        const mla_m4_tensor * mask, float kq_scale, const mla_m4_tensor * dst, void * stream);
 
 /* Split count mla_m4_kqkv uses for a decode window of n_kv keys (a function of the window). */
 int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type);
