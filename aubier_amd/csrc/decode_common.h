@@ -21,7 +21,8 @@ constexpr int NWAVE = 4;
 constexpr int NTHR = 64 * NWAVE;
 constexpr int WK = TK / NWAVE;  // keys per wave slice
 constexpr int HG = 32;          // heads per workgroup
-constexpr float LAZY = 8.0f;    // log2 slack before a reference max moves
+constexpr float LAZY = 15.0f;   // log2 slack before a reference max moves: P = 2^(s - m) <= 2^15,
+                                // exact in f16 (max 65504); a move rescales every accumulator
 // The lazily moved reference max of a head with no live key yet: below every finite score, so a
 // live key always moves it and exp2(s - M_NONE) of a masked key (s = -inf) is 0 without a special
 // case; a head still at M_NONE after the split had no live key (recorded as -inf).
@@ -509,7 +510,7 @@ __device__ __forceinline__ void decode_epilogue(const DecodeArgs & a, char * rin
 
     // ---- per head: l over all keys of the split, relative to the common reference m_ref ----
     // Every wave summed the whole P exchange for its heads, so each finishes on its own: no
-    // workgroup barrier from here on.  The header is (m_ref, l): m_ref lies within 2^8 below the
+    // workgroup barrier from here on.  The header is (m_ref, l): m_ref lies within 2^15 below the
     // split's max, which the merge's algebra does not care about (only m + ln l enters it).
     const float L = halves_sum(l_acc);         // head lane_e & 31
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;

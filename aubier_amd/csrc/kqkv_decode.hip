@@ -9,7 +9,7 @@
 //     60 FLOP per cache byte): they run on v_mfma_f32_16x16x32_f16 / v_mfma_f32_32x32x16_f16 with
 //     f32 accumulation.  q enters the MFMA as f16, where the unfused ggml-cpu graph rounds it (its
 //     mul_mat converts src1 to F16 for an F16 src0).  P enters as f16 as well, but UNNORMALISED
-//     (exp2 of the score minus the lazy reference max below, at most 2^8), whereas ggml-cpu rounds
+//     (exp2 of the score minus the lazy reference max below, at most 2^15), whereas ggml-cpu rounds
 //     the normalised softmax output to f16; at long context that is subnormal in f16, so the two
 //     rounding points differ (this kernel is the closer of the two to exact arithmetic).
 //   * Work split of a 64-key tile over the 4 waves (one per SIMD): for Q.K^T wave w owns its slice,
@@ -19,8 +19,8 @@
 //     through a 4.5 KB LDS exchange; that and the slice maxima need one workgroup barrier per tile,
 //     and the end of the split needs none, which keeps the tail after the last tile short.
 //   * Online softmax in log2 units (v_exp_f32) against a reference max shared by the waves and
-//     moved lazily: only when a tile raises a head's max by more than 2^8, so P = exp2(s - m_ref)
-//     <= 256 (exact range in f16) and the accumulator rescale is rare.  P is computed against the
+//     moved lazily: only when a tile raises a head's max by more than 2^15, so P = exp2(s - m_ref)
+//     <= 32768 (exact range in f16) and the accumulator rescale is rare.  P is computed against the
 //     current reference before the barrier and recomputed after it only when the reference moves.
 //   * l is summed from the same f16 P values the P.V MFMAs consume (every wave reads the whole P
 //     exchange for its heads), so o / l is an exact convex combination of V rows and each wave

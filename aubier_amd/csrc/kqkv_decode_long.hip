@@ -11,7 +11,7 @@
 //     (P^T[16 keys x 32 heads]) with two v_permlane16_swap, and P.V runs as o^T = V^T . P^T, so
 //     every accumulator column is one head and the softmax rescale is a per-lane scalar.
 //   * Online softmax in log2 units against a per-wave reference max moved lazily (only when a
-//     slice raises a head's max by more than 2^8: P = exp2(s - m) <= 256, exact range in f16, and
+//     slice raises a head's max by more than 2^15: P = exp2(s - m) <= 32768, exact range in f16, and
 //     the accumulator rescale is rare).  l is summed from the same f16 P values the MFMAs consume.
 //
 // Grid = (n_split, ceil(H/32), nt), 256 threads; output as kqkv_decode.hip.
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_long_kernel(DecodeArg
                 asm volatile("s_nop 7" ::: "memory");
             }
         }
-        // P = 2^(s - m) <= 2^8 in f16; lane (j16, g) holds keys 4 g .. 4 g + 3 of heads j16 (x) and
+        // P = 2^(s - m) <= 2^15 in f16; lane (j16, g) holds keys 4 g .. 4 g + 3 of heads j16 (x) and
         // 16 + j16 (y).  Swapping the odd 16-lane rows of x with the even rows of y leaves lane l
         // with head l & 31, keys 8 (l >> 5) .. +7 in (x, y): the P^T operand of P.V.
         uint32_t px[2], py[2];

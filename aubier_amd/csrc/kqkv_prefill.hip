@@ -16,11 +16,11 @@
 //     slices.
 //   * Per slice: S^T = K . Q^T (16 keys x 32 heads, v_mfma_f32_16x16x32_f16, accumulators in
 //     VGPRs: the output tiles fill the AGPRs), scores with the token's mask, a lazily moved
-//     reference max (P = exp2(s - m) <= 256; the move test on each lane's own maxima), P^T for P.V
+//     reference max (P = exp2(s - m) <= 2^15; the move test on each lane's own maxima), P^T for P.V
 //     by two v_permlane16_swap, o^T += V^T . P^T (v_mfma_f32_32x32x16_f16, V^T by
 //     ds_read_b64_tr_b16).  l is summed from the same f16 P values.  q enters as f16, where
 //     ggml-cpu's mul_mat rounds it; P enters as f16 too, but UNNORMALISED (exp2 of the score minus
-//     the lazy reference max, <= 256), where ggml-cpu rounds the normalised softmax output -- at
+//     the lazy reference max, <= 2^15), where ggml-cpu rounds the normalised softmax output -- at
 //     long context the latter is subnormal in f16, so the two differ by more than one rounding
 //     (this kernel is the closer of the two to exact arithmetic).  The next slice's first Q.K^T
 //     operands and mask values are read

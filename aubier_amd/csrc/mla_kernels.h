@@ -14,7 +14,7 @@ namespace mla {
 //   T      o[n_split][32][D_v]   split s's o / l
 // with
 //   m      a reference for the split's scores, natural-log units: the exact max (VALU kernel) or a
-//          running reference at most 8 ln 2 below it (MFMA kernels); -inf if the split is empty.
+//          running reference at most 15 ln 2 below it (MFMA kernels); -inf if the split is empty.
 //          The merge only uses m + ln l.
 //   l      sum_j exp(s_j - m)
 //   o / l  the split's normalised softmax output.  T is the cache's element type: f16 for an f16

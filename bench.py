@@ -39,6 +39,7 @@ METRIC = "µs/decode-step + achieved HBM GB/s (% peak) for MLA attention at 32K 
 HBM_PEAK_GBPS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 COLD_BYTES = 512 << 20         # bytes one rotation of step inputs must exceed (2 x the MALL)
+GRAPH_MIN_STEPS = 64           # steps per captured graph, at least
 CAL_BYTES = 256 << 20          # calibration copy size (each way) for the HBM traffic counters
 TRAFFIC_FILES = {3: ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",      # per decode config
                  4: ROOT / "profiles" / "kqkv_decode_long_cfg4_traffic.json"}
@@ -67,8 +68,8 @@ def cpu_threads() -> dict:
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=240)
-    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--steps", type=int, default=288)
+    ap.add_argument("--warmup", type=int, default=72)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--splits", type=int, default=0, help="split count (0 = library default)")
     ap.add_argument("--batch", type=int, default=0,
@@ -111,6 +112,9 @@ class Decode:
         kc_bytes = inp.n_kv * DK * es
         per_step = kc_bytes + H * DV * I.D_NOPE * 4
         self.n_rot = max(12, math.ceil(COLD_BYTES / per_step))
+        # steps per captured graph: whole rotations, at least GRAPH_MIN_STEPS (a graph replay costs
+        # ~6 us of its own, which an engine spreads over a whole forward pass of many layers)
+        self.glen = self.n_rot * math.ceil(GRAPH_MIN_STEPS / self.n_rot)
         kc0 = torch.from_numpy(np.ascontiguousarray(inp.kcache)).to(dev)
         wkb0 = torch.from_numpy(inp.w_kb).to(dev)
         q = np.concatenate([inp.q_nope, inp.q_pe], axis=2).astype(np.float32)
@@ -178,26 +182,26 @@ class Decode:
         return e0.elapsed_time(e1) * 1000.0 / (reps * per)
 
     def run_steps(self, k, warmup, step=None):
-        """Exactly `warmup` untimed then exactly `k` timed steps (whole rotations replayed as one
-        graph, the remainder as another); returns (us per step, wall seconds of the timed region)."""
+        """Exactly `warmup` untimed then exactly `k` timed steps (graphs of glen steps, the
+        remainder as one more graph); returns (us per step, wall seconds of the timed region)."""
         torch = self.torch
         step = step or self.step
-        g_full = self.capture(step, self.n_rot)
+        g_full = self.capture(step, self.glen)
         g_rem = {}
 
         def replay_n(n):
-            for _ in range(n // self.n_rot):
+            for _ in range(n // self.glen):
                 g_full.replay()
-            r = n % self.n_rot
+            r = n % self.glen
             if r:
                 if r not in g_rem:
                     g_rem[r] = self.capture(step, r)
                 g_rem[r].replay()
 
-        if k % self.n_rot:
-            g_rem[k % self.n_rot] = self.capture(step, k % self.n_rot)
-        if warmup % self.n_rot and warmup % self.n_rot not in g_rem:
-            g_rem[warmup % self.n_rot] = self.capture(step, warmup % self.n_rot)
+        if k % self.glen:
+            g_rem[k % self.glen] = self.capture(step, k % self.glen)
+        if warmup % self.glen and warmup % self.glen not in g_rem:
+            g_rem[warmup % self.glen] = self.capture(step, warmup % self.glen)
         torch.cuda.synchronize()
         replay_n(warmup)
         torch.cuda.synchronize()
@@ -212,20 +216,20 @@ class Decode:
 
     def per_kernel(self, reps):
         """Per-launch us of each kernel: graphs of back-to-back launches (COLD)."""
-        n = self.n_rot
+        n = self.glen
         return {"wkb": self.time_graph(self.capture(self.wkb, n), reps, n),
                 "partial": self.time_graph(self.capture(self.attn, n), reps, n),
                 "merge": self.time_graph(self.capture(lambda i: self.merge(), n), reps, n)}
 
     def warm_step(self, reps):
-        return self.time_graph(self.capture(lambda i: self.step(0), self.n_rot), reps, self.n_rot)
+        return self.time_graph(self.capture(lambda i: self.step(0), self.glen), reps, self.glen)
 
     def split_sweep(self, reps):
         res = {}
         for S in (64, 128, 192, 256):
             p = self.new_part(S)
-            ua = self.time_graph(self.capture(lambda i, p=p, S=S: self.attn(i, p, S), self.n_rot), reps, self.n_rot)
-            um = self.time_graph(self.capture(lambda i, p=p: self.merge(p), self.n_rot), reps, self.n_rot)
+            ua = self.time_graph(self.capture(lambda i, p=p, S=S: self.attn(i, p, S), self.glen), reps, self.glen)
+            um = self.time_graph(self.capture(lambda i, p=p: self.merge(p), self.glen), reps, self.glen)
             res[str(S)] = {"us_partial": round(ua, 3), "us_merge": round(um, 3),
                            "partial_GBps": round(self.bytes_attn / (ua * 1e3), 1)}
         return res
@@ -257,7 +261,7 @@ def decode_timings(d, steps, warmup, reps, sweep):
     us_step, wall = d.run_steps(steps, warmup)
     k = d.per_kernel(reps)
     r = {"n_kv": d.W, "nt": d.inp.nt, "splits": d.S, "cache": "f16" if d.inp.kc_f16 else "f32",
-         "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot,
+         "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot, "steps_per_graph": d.glen,
          "us_step": round(us_step, 3), "wall_s_timed": round(wall, 6),
          "us_wkb": round(k["wkb"], 3), "us_kqkv_partial": round(k["partial"], 3), "us_phase_merge": round(k["merge"], 3),
          "alg_bytes_step": int(d.bytes_step),

@@ -74,7 +74,7 @@ enum {
  * for an F32 cache):
  *   float2 ml[32][n_split]      (m, l) of head h, split s at [h][s]:
  *                               m  a reference for the split's scaled, masked scores (natural-log
- *                                  units, at most 8 ln 2 below their max; -INFINITY for a split
+ *                                  units, at most 15 ln 2 below their max; -INFINITY for a split
  *                                  with no live key) -- the merge only uses m + ln l
  *                               l  sum over the split's keys of exp(score - m)
  *   T      o[n_split][32][D_v]  o / l: the split's normalised softmax output; T = f16 for an
@@ -125,7 +125,7 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
  *   dst[h][t][:] = softmax_j(kq_scale * q[t][h].K[j] + mask[t][j]) . V[j][:]
  * An F16 cache runs on MFMA with q rounded to f16 where the unfused ggml-cpu graph rounds it (its
  * mul_mat converts src1 to F16 for an F16 src0) and P rounded to f16 UNNORMALISED (exp2 of the
- * score minus a running reference max, at most 2^8) -- ggml-cpu rounds the normalised P instead,
+ * score minus a running reference max, at most 2^15) -- ggml-cpu rounds the normalised P instead,
  * which is subnormal in f16 at long context, so results differ from the oracle by more than one
  * rounding there (and are closer to exact arithmetic); an F32 cache runs in f32.
  * nt == 1 is split-K decode (partial + merge, two launches); nt > 1 is the prefill path.

@@ -25,6 +25,29 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "kqkv_bench_pattern.npz"
 TILES_SHORT_MAX = 6   # splits of more tiles take the independent-wave kernel
+LAZY_LOG2 = 15.0      # the kernels move a head's reference max when a tile or slice beats it by more
+
+
+def reference_moves(kc, q, mask, scale, n_split, tile=64):
+    """How many times, summed over heads and splits, a 64-key tile's max score beats the running
+    reference by more than LAZY_LOG2 (the first live tile of a split sets it): the accumulator
+    rescales the sharp inputs must exercise (the kernels test at 64- or 16-key granularity)."""
+    n_kv = kc.shape[0]
+    sc = (q[0].astype(np.float64) @ kc.astype(np.float64).T) * scale * np.log2(np.e)
+    sc = np.where(np.isneginf(mask[0])[None, :], -np.inf, sc)
+    n_tiles = (n_kv + tile - 1) // tile
+    base, rem = divmod(n_tiles, n_split)
+    moves = 0
+    t0 = 0
+    for sp in range(n_split):
+        nt_ = base + (1 if sp < rem else 0)
+        ref = np.full(sc.shape[0], -np.inf)
+        for t in range(t0, t0 + nt_):
+            tm = sc[:, t * tile:(t + 1) * tile].max(axis=1)
+            moves += int(np.sum(np.isfinite(ref) & (tm > ref + LAZY_LOG2)))
+            ref = np.where(np.isneginf(ref) | (tm > ref + LAZY_LOG2), tm, ref)
+        t0 += nt_
+    return moves
 
 
 def check(name, got, ref, abs_tol, rel_tol):
@@ -82,10 +105,10 @@ def make_inputs(dev, dk, n_kv, H=32, seed=7100, q_scale=0.05, holes=False):
 ])
 @pytest.mark.parametrize("sharp", [False, True])
 def test_short_and_long_kernels_agree_with_oracle(dev, dk, dv, n_kv, splits, sharp):
-    """sharp: q drawn with scale 100 (scores with a spread of ~12 log2 units), so the lazy
-    reference maxima move and the accumulators are rescaled mid-split; with masked holes and a
-    masked tail."""
-    kc, q, mask, kc_d, q_d, m_d = make_inputs(dev, dk, n_kv, q_scale=100.0 if sharp else 0.05, holes=sharp)
+    """sharp: q drawn with scale 300 (scores with a standard deviation of ~37 log2 units), so the
+    lazy reference maxima move and the accumulators are rescaled mid-split (counted below); with
+    masked holes and a masked tail."""
+    kc, q, mask, kc_d, q_d, m_d = make_inputs(dev, dk, n_kv, q_scale=300.0 if sharp else 0.05, holes=sharp)
     scale = float(np.float32(1.0 / np.sqrt(192.0)))
     ref = orc.kqkv(kc, q, mask, scale, d_v=dv)
     ref64 = orc.attn_f64(kc, q[:, :4], mask, scale, d_v=dv)
@@ -94,6 +117,10 @@ def test_short_and_long_kernels_agree_with_oracle(dev, dk, dv, n_kv, splits, sha
     for S in splits:
         tps = (n_tiles + S - 1) // S
         kind = "long" if tps > TILES_SHORT_MAX else "short"
+        if sharp:
+            mv = reference_moves(kc, q, mask, scale, S)
+            say(f"S={S}: {mv} reference moves after a split's first live tile")
+            assert mv > 0
         out = run_split(kc_d, q_d, m_d, scale, S, dv)
         outs[S] = out
         rel = 2e-2 if sharp else 3e-3
