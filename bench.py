@@ -354,7 +354,7 @@ def main() -> int:
                 continue
             ic = I.make_config(cfg)
             if ic.nt > 1:
-                others[str(cfg)] = prefill_record(ic, 16, 4, cpu=not args.no_cpu, cpu_thr=thr["threads"], nested=True)
+                others[str(cfg)] = prefill_record(ic, 48, 8, cpu=not args.no_cpu, cpu_thr=thr["threads"], nested=True)
             else:
                 others[str(cfg)] = decode_record(ic, args, steps=48, warmup=12, reps=4, sweep=False,
                                                  cpu_runs=0 if args.no_cpu else 3, cpu_thr=thr["threads"])
@@ -463,12 +463,14 @@ def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = F
     n_split = max(1, need // (((H + 31) // 32) * T * A.ops.part_floats(DV) * 4)) if need else 1
     if n_split > 1:
         part = torch.empty(((H + 31) // 32, T, n_split, A.ops.part_floats(DV, inp.kc_f16)), dtype=torch.float32, device=dev)
-    us_wkb = time_fn(lambda: A.ggml_m4_wkb(wkb_w, qd[:, :, :I.D_NOPE], out=qcur[:, :, :DV]), 3)
+    # per kernel: 12 replays of a 4-launch graph (fewer read low right after another config's run)
+    KR = 12
+    us_wkb = time_fn(lambda: A.ggml_m4_wkb(wkb_w, qd[:, :, :I.D_NOPE], out=qcur[:, :, :DV]), KR)
     if part is not None:
-        us_attn = time_fn(lambda: A.ggml_m4_kqkv_partial(kc, qcur, mask, inp.kq_scale, n_split, part=part), 3)
-        us_merge = time_fn(lambda: A.ggml_m4_phase_merge(part, out=out), 3)
+        us_attn = time_fn(lambda: A.ggml_m4_kqkv_partial(kc, qcur, mask, inp.kq_scale, n_split, part=part), KR)
+        us_merge = time_fn(lambda: A.ggml_m4_phase_merge(part, out=out), KR)
     else:
-        us_attn = time_fn(lambda: A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws), 3)
+        us_attn = time_fn(lambda: A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws), KR)
         us_merge = 0.0
     step()
     torch.cuda.synchronize()
