@@ -213,64 +213,76 @@ __device__ __forceinline__ void write_empty_pairs(const DecodeArgs & a, int g, i
     }
 }
 
+// q block DMA: this wave's share of the 32 heads x DK f32 q rows of token t into the staging area
+// at LDS address qsb, f32 chunk c of head h at slot h * QC + (c ^ (h & 15)) (so that the fragment
+// reads of q_convert, 16 heads at one chunk, hit distinct banks); heads past n_head read as zeros.
+// QD instructions per wave.
+template <int DK>
+__device__ __forceinline__ void q_dma(const DecodeArgs & a, uint32_t qsb, int hg0, int t, int w, int lane) {
+    using G = SliceGeom<DK>;
+    const int nh = min(HG, a.n_head - hg0);
+    const i32x4 qrs = make_rsrc(reinterpret_cast<const char *>(a.q) + (size_t)t * a.q_nb2 + (size_t)hg0 * a.q_nb1,
+                                (uint32_t)((int64_t)(nh - 1) * a.q_nb1 + DK * 4));
+#pragma unroll
+    for (int i = 0; i < G::QD; ++i) {
+        const int p = (w * G::QD + i) * 64 + lane;
+        const int h = p / G::QC;
+        const int c = (p - h * G::QC) ^ (h & 15);
+        dma16(qrs, (uint32_t)(h * a.q_nb1) + 16u * (uint32_t)c, 0u, qsb + (uint32_t)((w * G::QD + i) * 1024));
+    }
+}
+
+// The staged q block (q_dma's layout at qs) -> f16 B fragments in registers: qreg[n][s] = head
+// 16 n + j16, d = 32 s + 8 g .. +7.
+template <int DK>
+__device__ __forceinline__ void q_convert(const char * qs_lds, int lane, half8 (&qreg)[2][SliceGeom<DK>::QSTEPS]) {
+    using G = SliceGeom<DK>;
+    const int g = lane >> 4, j16 = lane & 15;
+    // reads in batches of QB fragments ahead of their conversion (a read-convert chain per
+    // fragment would serialise on the LDS latency)
+    constexpr int QB = G::QSTEPS % 6 == 0 ? 6 : (G::QSTEPS % 5 == 0 ? 5 : 2);
+    static_assert(G::QSTEPS % QB == 0, "whole batches");
+    const float * qs = reinterpret_cast<const float *>(qs_lds);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        const float * row = qs + 4 * (16 * n + j16) * G::QC;
+#pragma unroll
+        for (int s0 = 0; s0 < G::QSTEPS; s0 += QB) {
+            f32x4 x[QB][2];
+#pragma unroll
+            for (int b = 0; b < QB; ++b) {
+                x[b][0] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g) ^ j16));
+                x[b][1] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g + 1) ^ j16));
+            }
+#pragma unroll
+            for (int b = 0; b < QB; ++b) {
+                half8 h = {to_half(x[b][0][0]), to_half(x[b][0][1]), to_half(x[b][0][2]), to_half(x[b][0][3]),
+                           to_half(x[b][1][0]), to_half(x[b][1][1]), to_half(x[b][1][2]), to_half(x[b][1][3])};
+                // materialise the f16 fragment here: left alone, the compiler keeps the f32
+                // values (twice the registers) and re-converts them at every use in the loop
+                asm volatile("" : "+v"(h));
+                qreg[n][s0 + b] = h;
+            }
+        }
+    }
+}
+
 // q block (32 heads x DK f32) -> stage 1 of the ring by DMA, tile 0's slice -> stage 0 behind it,
-// then f16 B fragments in registers: qreg[n][s] = head 16 n + j16, d = 32 s + 8 g .. +7.  Staging
-// slot of f32 chunk c (4 floats) of head h: h * QC + (c ^ (h & 15)), so the fragment reads (16
-// heads, one chunk) hit distinct banks; heads past n_head read as zeros.  Ends with a barrier
-// after which stage 1 is free; the slice DMA of tile 0 (DMA_N + 1 instructions) may still be in flight.
+// then f16 B fragments in registers (q_convert).  Ends with a barrier after which stage 1 is free;
+// the slice DMA of tile 0 (DMA_N + 1 instructions) may still be in flight.
 template <int DK>
 __device__ __forceinline__ void stage_q(const DecodeArgs & a, const SliceStream<DK> & ss, char * ring, int hg0, int t,
                                         int lane, half8 (&qreg)[2][SliceGeom<DK>::QSTEPS]) {
     using G = SliceGeom<DK>;
-    const int w = ss.w;
-    const int g = lane >> 4, j16 = lane & 15;
+    q_dma<DK>(a, ss.ring_lds + (uint32_t)(NWAVE * G::STAGE), hg0, t, ss.w, lane);
     {
-        const int nh = min(HG, a.n_head - hg0);
-        const i32x4 qrs = make_rsrc(reinterpret_cast<const char *>(a.q) + (size_t)t * a.q_nb2 + (size_t)hg0 * a.q_nb1,
-                                    (uint32_t)((int64_t)(nh - 1) * a.q_nb1 + DK * 4));
-        const uint32_t qsb = ss.ring_lds + (uint32_t)(NWAVE * G::STAGE);
-#pragma unroll
-        for (int i = 0; i < G::QD; ++i) {
-            const int p = (w * G::QD + i) * 64 + lane;
-            const int h = p / G::QC;
-            const int c = (p - h * G::QC) ^ (h & 15);
-            dma16(qrs, (uint32_t)(h * a.q_nb1) + 16u * (uint32_t)c, 0u, qsb + (uint32_t)((w * G::QD + i) * 1024));
-        }
         const SliceDma d0 = ss.plan(0, 0);
 #pragma unroll
         for (int i = 0; i <= G::DMA_N; ++i) ss.put(d0, i);
     }
     wait_vm<G::DMA_N + 1>();                 // this wave's part of q has landed
     __syncthreads();
-    {
-        // reads in batches of QB fragments ahead of their conversion (a read-convert chain per
-        // fragment would serialise on the LDS latency)
-        constexpr int QB = G::QSTEPS % 6 == 0 ? 6 : (G::QSTEPS % 5 == 0 ? 5 : 2);
-        static_assert(G::QSTEPS % QB == 0, "whole batches");
-        const float * qs = reinterpret_cast<const float *>(ring + NWAVE * G::STAGE);
-#pragma unroll
-        for (int n = 0; n < 2; ++n) {
-            const float * row = qs + 4 * (16 * n + j16) * G::QC;
-#pragma unroll
-            for (int s0 = 0; s0 < G::QSTEPS; s0 += QB) {
-                f32x4 x[QB][2];
-#pragma unroll
-                for (int b = 0; b < QB; ++b) {
-                    x[b][0] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g) ^ j16));
-                    x[b][1] = *reinterpret_cast<const f32x4 *>(row + 4 * ((8 * (s0 + b) + 2 * g + 1) ^ j16));
-                }
-#pragma unroll
-                for (int b = 0; b < QB; ++b) {
-                    half8 h = {to_half(x[b][0][0]), to_half(x[b][0][1]), to_half(x[b][0][2]), to_half(x[b][0][3]),
-                               to_half(x[b][1][0]), to_half(x[b][1][1]), to_half(x[b][1][2]), to_half(x[b][1][3])};
-                    // materialise the f16 fragment here: left alone, the compiler keeps the f32
-                    // values (twice the registers) and re-converts them at every use in the loop
-                    asm volatile("" : "+v"(h));
-                    qreg[n][s0 + b] = h;
-                }
-            }
-        }
-    }
+    q_convert<DK>(ring + NWAVE * G::STAGE, lane, qreg);
     __syncthreads();                         // the q staging in stage 1 is free again
 }
 
@@ -498,7 +510,7 @@ __device__ __forceinline__ void pv_tile(const char * ring, const half_t * pxv, i
 // by wave 0, o / l in f16 through this wave's slot of the ring stage the last tile did not use).
 // No workgroup barrier: every wave holds its own heads' l.
 template <int DK, int DV>
-__device__ __forceinline__ void decode_epilogue(const DecodeArgs & a, char * ring, int n_my, int w, int tid, int t, int hg0,
+__device__ __forceinline__ void decode_epilogue(const DecodeArgs & a, char * stg, int w, int tid, int t, int hg0,
                                                 int sp, f32x16 (&o)[ShortCfg<DK, DV>::NTQ], float l_acc,
                                                 const float (&m_ref)[2]) {
     using C = ShortCfg<DK, DV>;
@@ -537,11 +549,9 @@ __device__ __forceinline__ void decode_epilogue(const DecodeArgs & a, char * rin
         *reinterpret_cast<f32x2 *>(rec + part_ml_off(a.n_split, lane_e, sp)) =
             f32x2{(mr == M_NONE) ? -INFINITY : mr * LN2, L};                      // m in natural-log units
     }
-    // o / l in f16 through this wave's own slot of the stage the last tile did not use (no wave
-    // reads it any more: the last tile's loop-top barrier follows every P.V of the one before),
-    // as [32 heads][DVQ] rows; then 16-byte chunks out, 4 head rows of 2 * DVQ bytes per
-    // instruction (whole cache lines).  Write and read are the same wave's, in LDS order.
-    char * stg = ring + stage_byte<DK>(n_my & 1, w);
+    // o / l in f16 through stg, LDS of this wave's own that no wave reads any more (at least
+    // HG * OPITCH bytes), as [32 heads][DVQ] rows; then 16-byte chunks out, 4 head rows of 2 * DVQ
+    // bytes per instruction (whole cache lines).  Write and read are the same wave's, in LDS order.
 #pragma unroll
     for (int i = 0; i < C::NTQ; ++i)
 #pragma unroll

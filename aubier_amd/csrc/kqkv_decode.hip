@@ -151,7 +151,9 @@ __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds
     }
     wait_vm<0>();                            // nothing of this wave may still target the ring
 
-    decode_epilogue<DK, DV>(a, ring, n_my, w, tid, t, hg0, sp, o, l_acc, m_ref);
+    // staging: this wave's slot of the stage the last tile did not use (no wave reads it any more:
+    // the last tile's loop-top barrier follows every P.V of the one before)
+    decode_epilogue<DK, DV>(a, ring + stage_byte<DK>(n_my & 1, w), w, tid, t, hg0, sp, o, l_acc, m_ref);
 }
 
 // ROWS = false: row blockIdx.z (one token, the plain decode step).  ROWS = true: rows blockIdx.z,

@@ -63,6 +63,10 @@ constexpr int PREFILL_MIN_TOKENS = 16;
 constexpr int PREFILL_TOKENS_PER_WG = 4;
 hipError_t launch_kqkv_prefill_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
 bool decode_f16_supported(int dk, int dv);
+// An 8-bit cache (ggml block_q8_0 rows, contiguous): the decode kernel of kqkv_decode_q8.hip, grid
+// (n_split, ceil(H/32), nt), the f16 path's partial records (f16 o) and direct output.
+hipError_t launch_kqkv_decode_q8(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
+inline bool decode_q8_supported(int dk, int dv) { return (dk == 576 && dv == 512) || (dk == 320 && dv == 256); }
 
 // Generic VALU path (f32 or f16 cache, any D_k <= 1024, D_v <= D_k): one workgroup per
 // (split, head, token).  round16 applies the f16 rounding of q and P (F16 cache semantics).

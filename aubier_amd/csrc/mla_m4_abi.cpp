@@ -68,13 +68,20 @@ bool al4(const void * p, bool plan) { return (plan && !p) || (reinterpret_cast<u
 int check_kqkv(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_tensor * mask,
                const mla_m4_tensor * dst, KqkvShape * s, bool plan = false) {
     if (!has_data(kc, plan) || !has_data(q, plan) || !has_data(dst, plan)) return MLA_M4_ERR_NULL;
-    if (kc->type != MLA_M4_TYPE_F16 && kc->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
+    const bool q8 = kc->type == MLA_M4_TYPE_Q8_0;
+    if (kc->type != MLA_M4_TYPE_F16 && kc->type != MLA_M4_TYPE_F32 && !q8) return MLA_M4_ERR_TYPE;
     if (q->type != MLA_M4_TYPE_F32 || dst->type != MLA_M4_TYPE_F32) return MLA_M4_ERR_TYPE;
-    const size_t es = elsize(kc->type);
     // kcache ne [D_k, n_kv, 1, 1]
     if (kc->ne[0] < 1 || kc->ne[1] < 1 || kc->ne[2] != 1 || kc->ne[3] != 1) return MLA_M4_ERR_SHAPE;
-    if (kc->nb[0] != es || kc->nb[1] < (size_t)kc->ne[0] * es || (kc->nb[1] & 15u) || !al16(kc->data, plan))
-        return MLA_M4_ERR_STRIDE;
+    if (q8) {
+        // ggml block_q8_0 rows (34-byte blocks of 32 values), contiguous
+        if (kc->ne[0] % 32) return MLA_M4_ERR_SHAPE;
+        if (kc->nb[0] != 34 || kc->nb[1] != (size_t)(kc->ne[0] / 32 * 34) || !al16(kc->data, plan)) return MLA_M4_ERR_STRIDE;
+    } else {
+        const size_t es = elsize(kc->type);
+        if (kc->nb[0] != es || kc->nb[1] < (size_t)kc->ne[0] * es || (kc->nb[1] & 15u) || !al16(kc->data, plan))
+            return MLA_M4_ERR_STRIDE;
+    }
     // q ne [D_k, H, nt, 1]
     if (q->ne[0] != kc->ne[0] || q->ne[1] < 1 || q->ne[2] < 1 || q->ne[3] != 1) return MLA_M4_ERR_SHAPE;
     if (q->nb[0] != 4 || (q->nb[1] & 15u) || (q->nb[2] & 15u) || !al16(q->data, plan)) return MLA_M4_ERR_STRIDE;
@@ -94,6 +101,10 @@ int check_kqkv(const mla_m4_tensor * kc, const mla_m4_tensor * q, const mla_m4_t
     }
     if (kc->ne[1] > INT32_MAX || q->ne[1] > 65535 || q->ne[2] > 65535) return MLA_M4_ERR_UNSUPPORTED;
     if (kc->ne[0] > 1024 || dv > 1024) return MLA_M4_ERR_UNSUPPORTED;
+    // the 8-bit cache runs on its MFMA kernel only: its two geometries, rows within 4 GiB
+    if (q8 && !(mla::decode_q8_supported((int)kc->ne[0], (int)dv) &&
+                (uint64_t)kc->ne[1] * (uint64_t)kc->nb[1] <= 0xFFFFFFFFull))
+        return MLA_M4_ERR_UNSUPPORTED;
     s->dk = kc->ne[0];
     s->dv = dv;
     s->n_kv = kc->ne[1];
@@ -116,11 +127,14 @@ bool use_mfma(const KqkvShape & s) {
 // several tokens on the MFMA path: the prefill kernel (4 tokens per workgroup share each tile)
 bool use_prefill(const KqkvShape & s) { return use_mfma(s) && s.nt >= mla::PREFILL_MIN_TOKENS; }
 
+// an 8-bit (Q8_0) cache: its own MFMA kernel, one workgroup per (split, head group, token)
+bool use_q8(const KqkvShape & s) { return s.kc_type == MLA_M4_TYPE_Q8_0; }
+
 int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
 
 int default_splits(const KqkvShape & s) {
     // the unit a split is made of: 64-key tiles (MFMA kernels), 16-key granules (VALU kernel)
-    const int64_t tiles = use_mfma(s) ? n_tiles_of(s.n_kv) : (s.n_kv + mla::GRAN_KEYS - 1) / mla::GRAN_KEYS;
+    const int64_t tiles = (use_mfma(s) || use_q8(s)) ? n_tiles_of(s.n_kv) : (s.n_kv + mla::GRAN_KEYS - 1) / mla::GRAN_KEYS;
     int64_t groups;   // workgroups per split
     if (use_prefill(s))
         groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) *
@@ -128,6 +142,7 @@ int default_splits(const KqkvShape & s) {
     // decode kernels: the rows of a split share its workgroup (the launch adds row groups only
     // when there are few splits), so the split count is the single-row one
     else if (use_mfma(s)) groups = (s.n_head + DECODE_HEADS - 1) / DECODE_HEADS;
+    else if (use_q8(s)) groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) * s.nt;
     else groups = s.n_head * s.nt;
     int64_t sp = (TARGET_WG + groups - 1) / groups;
     if (sp > tiles) sp = tiles;
@@ -138,7 +153,7 @@ int default_splits(const KqkvShape & s) {
 
 int64_t n_groups_of(int64_t n_head) { return (n_head + MLA_M4_PART_HEADS - 1) / MLA_M4_PART_HEADS; }
 
-int part_o_bytes(const KqkvShape & s) { return s.kc_type == MLA_M4_TYPE_F16 ? 2 : 4; }
+int part_o_bytes(const KqkvShape & s) { return s.kc_type == MLA_M4_TYPE_F32 ? 4 : 2; }     // f16 o for F16 and Q8_0 caches
 
 int64_t part_floats(const KqkvShape & s) { return (int64_t)(mla::part_block_bytes((int)s.dv, part_o_bytes(s)) / 4); }
 
@@ -169,7 +184,8 @@ mla::DecodeArgs make_args(const mla_m4_tensor * kc, const mla_m4_tensor * q, con
 
 int launch_attn(const KqkvShape & s, const mla::DecodeArgs & a, hipStream_t stream) {
     hipError_t e;
-    if (use_prefill(s)) e = mla::launch_kqkv_prefill_f16((int)s.dk, (int)s.dv, a, stream);
+    if (use_q8(s)) e = mla::launch_kqkv_decode_q8((int)s.dk, (int)s.dv, a, stream);
+    else if (use_prefill(s)) e = mla::launch_kqkv_prefill_f16((int)s.dk, (int)s.dv, a, stream);
     else if (use_mfma(s)) e = mla::launch_kqkv_decode_f16((int)s.dk, (int)s.dv, a, stream);
     else e = mla::launch_kqkv_generic((int)s.dk, (int)s.dv, s.kc_type == MLA_M4_TYPE_F16, a, stream);
     return e == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;

@@ -13,7 +13,7 @@ W_kb [H][D_v][d_n] = ggml ne [128, 512, 32] f32, kq_scale = 1/sqrt(192), mask 0 
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 from typing import Optional
 
 import numpy as np
@@ -84,6 +84,42 @@ class MlaInputs:
     kq_scale: float = KQ_SCALE
     seeds: dict = field(default_factory=dict)
     notes: str = ""
+    kcache_q8: Optional[np.ndarray] = None   # [W, 612] uint8: the cache in ggml block_q8_0 (with_q8_cache)
+
+
+def q8_0_rows(x: np.ndarray) -> np.ndarray:
+    """f32 rows [rows, ne0] -> ggml block_q8_0 bytes [rows, ne0 / 32 * 34] (the algorithm of ggml's
+    quantize_row_q8_0_ref: per 32 values d = amax / 127, the stored scale f16(d), q = roundf(x / d)
+    computed as x * (1 / d) in f32, half away from zero): the 8-bit latent cache of the Q8_0 KQKV
+    kernel, for synthetic caches."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, ne0 = x.shape
+    b = x.reshape(rows, ne0 // 32, 32)
+    d = (np.abs(b).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    x0 = (b * idv[:, :, None]).astype(np.float32).astype(np.float64)
+    q = np.sign(x0) * np.floor(np.abs(x0) + 0.5)
+    out = np.empty((rows, ne0 // 32, 34), dtype=np.uint8)
+    out[:, :, :2] = d.astype(np.float16).view(np.uint8).reshape(rows, ne0 // 32, 2)
+    out[:, :, 2:] = q.astype(np.int8).view(np.uint8)
+    return out.reshape(rows, ne0 // 32 * 34)
+
+
+def q8_0_rows_f16(w: np.ndarray, ne0: int) -> np.ndarray:
+    """block_q8_0 bytes -> the f16 values a Q8_0 kernel computes with, f16(q * d)."""
+    b = np.ascontiguousarray(w).reshape(w.shape[0], ne0 // 32, 34)
+    d = b[:, :, :2].copy().view(np.float16).astype(np.float32).reshape(w.shape[0], ne0 // 32, 1)
+    return (d * b[:, :, 2:].copy().view(np.int8).astype(np.float32)).reshape(w.shape[0], ne0).astype(np.float16)
+
+
+def with_q8_cache(inp: MlaInputs) -> MlaInputs:
+    """The same inputs with the cache quantised to ggml block_q8_0: kcache_q8 holds the bytes and
+    kcache the f16 values they stand for (so any f16-cache reference on kcache is the reference of
+    a Q8_0 kernel on kcache_q8)."""
+    wq = q8_0_rows(inp.kcache.astype(np.float32))
+    return replace(inp, kcache_q8=wq, kcache=q8_0_rows_f16(wq, inp.kcache.shape[1]), kc_f16=True,
+                   notes=(inp.notes + "; " if inp.notes else "") + "cache in Q8_0")
 
 
 def make_config(cfg: int, n_kv: Optional[int] = None, nt: Optional[int] = None) -> MlaInputs:

@@ -223,17 +223,33 @@ def kqkv_workspace_bytes(kcache: torch.Tensor, q: torch.Tensor, out: torch.Tenso
     return int(lib.mla_m4_kqkv_workspace_bytes(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(out))))
 
 
+def _kc_width(kcache) -> int:
+    """D_k of a cache: a torch tensor [n_kv, D_k] or a Q8_0 one (ne0)."""
+    return kcache.ne0 if isinstance(kcache, Q8_0) else kcache.shape[1]
+
+
+def _dv_of(kcache) -> int:
+    """D_v of the op's output for a cache of width D_k: 512 for the 576-wide cache, 256 for the
+    reference's 320-wide one, else D_k."""
+    dk = _kc_width(kcache)
+    return 512 if dk == 576 else (256 if dk == 320 else dk)
+
+
+def _kc_f16_partials(kcache) -> bool:
+    """Whether the partial records hold f16 o (F16 and Q8_0 caches) or f32 (F32 cache)."""
+    return isinstance(kcache, Q8_0) or kcache.dtype == torch.float16
+
+
 def ggml_m4_kqkv(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[torch.Tensor], kq_scale: float,
                  out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """GGML_OP_M4_KQKV: out[h, t, :] = softmax_j(kq_scale * q[t, h] . K[j] + mask[t, j]) . V[j, :D_v].
 
-    kcache [n_kv, D_k] f16/f32; q [nt, H, D_k] f32; mask [>= nt, n_kv] f32 or None;
+    kcache [n_kv, D_k] f16/f32, or Q8_0 (ne0 = D_k); q [nt, H, D_k] f32; mask [>= nt, n_kv] f32 or None;
     out [H, nt, D_v] f32 (D_v = 512 unless out is given).  workspace: optional uint8 device
     buffer (allocated here when None and the shape needs one)."""
     lib = load_library()
     if out is None:
-        dv = 512 if kcache.shape[1] == 576 else (256 if kcache.shape[1] == 320 else kcache.shape[1])
-        out = torch.empty((q.shape[1], q.shape[0], dv), dtype=torch.float32, device=q.device)
+        out = torch.empty((q.shape[1], q.shape[0], _dv_of(kcache)), dtype=torch.float32, device=q.device)
     vk, vq, vm, vo = view(kcache), view(q), view(mask), view(out)
     need = int(lib.mla_m4_kqkv_workspace_bytes(_ptr(vk), _ptr(vq), _ptr(vo)))
     if workspace is None and need > 0:
@@ -254,8 +270,7 @@ def ggml_m4_kqkv_noalloc(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[t
     (include/mla_m4.h mla_m4_kqkv_noalloc; calls that overlap on one GPU race)."""
     lib = load_library()
     if out is None:
-        dv = 512 if kcache.shape[1] == 576 else (256 if kcache.shape[1] == 320 else kcache.shape[1])
-        out = torch.empty((q.shape[1], q.shape[0], dv), dtype=torch.float32, device=q.device)
+        out = torch.empty((q.shape[1], q.shape[0], _dv_of(kcache)), dtype=torch.float32, device=q.device)
     _check("ggml_m4_kqkv_noalloc", lib.mla_m4_kqkv_noalloc(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(mask)),
                                                            ctypes.c_float(kq_scale), _ptr(view(out)), _stream(q)))
     return out
@@ -267,7 +282,7 @@ def ggml_m4_kqkv_partial(kcache: torch.Tensor, q: torch.Tensor, mask: Optional[t
     lib = load_library()
     if part is None:
         G = (q.shape[1] + PART_HEADS - 1) // PART_HEADS
-        part = torch.empty((G, q.shape[0], n_split, part_floats(d_v, kcache.dtype == torch.float16)),
+        part = torch.empty((G, q.shape[0], n_split, part_floats(d_v, _kc_f16_partials(kcache))),
                            dtype=torch.float32, device=q.device)
     _check("ggml_m4_kqkv_partial", lib.mla_m4_kqkv_partial(_ptr(view(kcache)), _ptr(view(q)), _ptr(view(mask)),
                                                            ctypes.c_float(kq_scale), int(n_split), int(d_v),

@@ -45,10 +45,13 @@ TRAFFIC_FILES = {3: ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",    
                  4: ROOT / "profiles" / "kqkv_decode_long_cfg4_traffic.json"}
 
 
-def partial_kernel_name(kc_f16: bool, n_kv: int, n_split: int) -> str:
+def partial_kernel_name(kc_f16: bool, n_kv: int, n_split: int, q8: bool = False) -> str:
     """The kernel the library launches for the split-K partial: an f16 cache takes the
     barrier-per-tile kernel for splits of at most 6 64-key tiles and the independent-wave kernel
-    for longer ones (launch_kqkv_decode_f16); an f32 cache takes the VALU kernel."""
+    for longer ones (launch_kqkv_decode_f16); an f32 cache takes the VALU kernel; a Q8_0 cache its
+    own kernel (launch_kqkv_decode_q8)."""
+    if q8:
+        return "kqkv_decode_q8_kernel<576,512>"
     if not kc_f16:
         return "kqkv_generic_kernel<f32 cache>"
     tiles_per_split = -(-(-(-n_kv // 64)) // n_split)
@@ -77,6 +80,9 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true", help="skip the S in {64,128,192,256} sweep")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true", help="time the headline config only")
+    ap.add_argument("--cache", choices=("f16", "q8"), default="f16",
+                    help="q8: the decode config's cache quantised to ggml Q8_0 (the 8-bit latent cache kernel); "
+                         "the CPU baseline and the errors use the f16 values it stands for")
     ap.add_argument("--ops", action="store_true",
                     help="time the reference-geometry quantised ops (Q8_0 WKB, PHASE wv_b, PHASE KV-write) instead")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -103,24 +109,28 @@ class Decode:
         dev = torch.device("cuda:0")
         H, DV, DK = I.N_HEAD, I.D_V, I.D_K
         self.H, self.DV, self.DK, self.W = H, DV, DK, inp.n_kv
+        self.q8 = inp.kcache_q8 is not None
         es = 2 if inp.kc_f16 else 4
         self.es = es
-        self.bytes_attn = inp.n_kv * (DK * es + 4) + inp.nt * H * DK * 4           # cache + mask + Qcur
+        row = DK // 32 * 34 if self.q8 else DK * es                                # cache bytes per key
+        self.bytes_attn = inp.n_kv * (row + 4) + inp.nt * H * DK * 4               # cache + mask + Qcur
         self.bytes_wkb = H * DV * I.D_NOPE * 4 + inp.nt * H * I.D_NOPE * 4 + inp.nt * H * DV * 4
         self.bytes_out = inp.nt * H * DV * 4
         self.bytes_step = self.bytes_attn + self.bytes_out + self.bytes_wkb
-        kc_bytes = inp.n_kv * DK * es
+        kc_bytes = inp.n_kv * row
         per_step = kc_bytes + H * DV * I.D_NOPE * 4
         self.n_rot = max(12, math.ceil(COLD_BYTES / per_step))
         # steps per captured graph: whole rotations, at least GRAPH_MIN_STEPS (a graph replay costs
         # ~6 us of its own, which an engine spreads over a whole forward pass of many layers)
         self.glen = self.n_rot * math.ceil(GRAPH_MIN_STEPS / self.n_rot)
-        kc0 = torch.from_numpy(np.ascontiguousarray(inp.kcache)).to(dev)
+        kc0 = torch.from_numpy(np.ascontiguousarray(inp.kcache_q8 if self.q8 else inp.kcache)).to(dev)
         wkb0 = torch.from_numpy(inp.w_kb).to(dev)
         q = np.concatenate([inp.q_nope, inp.q_pe], axis=2).astype(np.float32)
         q0 = torch.from_numpy(q).to(dev)
         self.mask = torch.from_numpy(inp.mask).to(dev)
         self.kcs = [kc0] + [kc0.clone() for _ in range(self.n_rot - 1)]
+        if self.q8:
+            self.kcs = [A.Q8_0(k, DK) for k in self.kcs]
         self.wkbs = [wkb0] + [wkb0.clone() for _ in range(self.n_rot - 1)]
         self.qs = [q0] + [q0.clone() for _ in range(self.n_rot - 1)]
         self.qcurs = []
@@ -128,7 +138,8 @@ class Decode:
             qc = torch.zeros((inp.nt, H, DK), dtype=torch.float32, device=dev)
             qc[:, :, DV:] = self.qs[i][:, :, I.D_NOPE:]
             self.qcurs.append(qc)
-        self.S = splits or A.default_splits(self.W, H, A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32)
+        self.S = splits or A.default_splits(self.W, H, A.ops.TYPE_Q8_0 if self.q8 else
+                                            (A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32))
         self.part = self.new_part(self.S)
         self.out = torch.empty((H, inp.nt, DV), dtype=torch.float32, device=dev)
         torch.cuda.synchronize()
@@ -260,20 +271,21 @@ def decode_timings(d, steps, warmup, reps, sweep):
     optionally the split sweep, and the dominant kernel's roofline."""
     us_step, wall = d.run_steps(steps, warmup)
     k = d.per_kernel(reps)
-    r = {"n_kv": d.W, "nt": d.inp.nt, "splits": d.S, "cache": "f16" if d.inp.kc_f16 else "f32",
+    r = {"n_kv": d.W, "nt": d.inp.nt, "splits": d.S, "cache": "q8_0" if d.q8 else ("f16" if d.inp.kc_f16 else "f32"),
          "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot, "steps_per_graph": d.glen,
          "us_step": round(us_step, 3), "wall_s_timed": round(wall, 6),
          "us_wkb": round(k["wkb"], 3), "us_kqkv_partial": round(k["partial"], 3), "us_phase_merge": round(k["merge"], 3),
          "alg_bytes_step": int(d.bytes_step),
+         "cache_bytes_per_key": (d.DK // 32 * 34 if d.q8 else d.DK * d.es) + 4,     # cache row + mask
          "step_GBps": round(d.bytes_step / (us_step * 1e3), 1),
          "step_frac_of_hbm_peak": round(d.bytes_step / (us_step * 1e3) / HBM_PEAK_GBPS, 4),
          "partial_GBps": round(d.bytes_attn / (k["partial"] * 1e3), 1),
          "partial_frac_of_hbm_peak": round(d.bytes_attn / (k["partial"] * 1e3) / HBM_PEAK_GBPS, 4),
          "wkb_GBps": round(d.bytes_wkb / (k["wkb"] * 1e3), 1),
-         "partial_kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S),
+         "partial_kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S, d.q8),
          "partial_bytes_written": int(d.part.numel() * 4),
          "warm_us_step": round(d.warm_step(reps), 3)}
-    r["roofline"] = {"kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S), "alg_bytes_per_launch": int(d.bytes_attn),
+    r["roofline"] = {"kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S, d.q8), "alg_bytes_per_launch": int(d.bytes_attn),
                      "us_per_launch": k["partial"], "timing": "graph of back-to-back launches"}
     if sweep:
         r["split_sweep"] = d.split_sweep(reps)
@@ -315,6 +327,8 @@ def main() -> int:
         inp = I.make_batch(args.batch, region, lens=[region] * args.batch)
     else:
         inp = I.make_config(args.config)
+        if args.cache == "q8" and inp.nt == 1:
+            inp = I.with_q8_cache(inp)
         if inp.nt > 1:
             rec = prefill_record(inp, args.steps, args.warmup, cpu=not args.no_cpu, cpu_thr=cpu_threads()["threads"])
             print(json.dumps(rec), flush=True)
@@ -347,7 +361,7 @@ def main() -> int:
         extra["err_vs_oracle"] = errors(out, ref)
 
     # ---- every other BASELINE config, timed the same way (fills the results table) ----
-    if not args.no_others and not args.batch:
+    if not args.no_others and not args.batch and args.cache == "f16":
         others = {}
         for cfg in (1, 2, 4, 5):
             if cfg == args.config:
@@ -379,7 +393,8 @@ def main() -> int:
         "config": {"workload": (f"batch-of-{inp.nt} decode: {inp.nt} rows x 32 heads, each over its own "
                                 f"{W // inp.nt}-cell region of one {W}-cell window, " if args.batch else
                                 f"config {args.config}: MLA decode, 1 token x 32 heads, {W} keys, ") +
-                               f"{'f16' if inp.kc_f16 else 'f32'} latent+rope cache [{W},576], W_kb f32 [32,512,128], "
+                               f"{'Q8_0 (ggml block_q8_0, 612 B/key)' if inp.kcache_q8 is not None else ('f16' if inp.kc_f16 else 'f32')} "
+                               f"latent+rope cache [{W},576], W_kb f32 [32,512,128], "
                                f"{step_desc} (S={S}), COLD ({extra['rotating_copies']} rotating copies), hipGraph",
                    "n_kv": W, "n_head": H, "d_k": I.D_K, "d_v": I.D_V, "splits": S, "seeds": inp.seeds, "notes": inp.notes},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

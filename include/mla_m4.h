@@ -118,6 +118,12 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
  * ggml_m4_kqkv (ggml.c:3429-3460), generalised:
  *   kcache F16|F32 ne [D_k, n_kv]    nb[0] = elsize, row stride nb[1] a multiple of 16 bytes;
  *                                     K = all D_k columns, V = columns [0, D_v) of the same row
+ *          or Q8_0 ne [D_k, n_kv]    an 8-bit cache (no counterpart in the reference, whose KQKV
+ *                                     asserts F16): ggml block_q8_0 rows (per 32 values an f16
+ *                                     scale d and 32 int8 q, value q d), contiguous (nb[1] =
+ *                                     D_k / 32 * 34), at (D_k, D_v) = (576, 512) or (320, 256);
+ *                                     computed as the F16 cache f16(q d) (the f32 product rounded
+ *                                     once), with the F16 path's numerics and f16 partials
  *   q      F32     ne [D_k, H, nt]   nb[0] = 4 (Qcur: absorbed nope part, then the rope part)
  *   mask   F32     ne [n_kv, >= nt]  nb[0] = 4 (0 / -INFINITY per key and token), or data NULL
  *   dst    F32     ne [D_v, nt, H]   contiguous

@@ -218,13 +218,48 @@ def q8_0_random(seed: int, rows: int, ne0: int, scale: float = 0.01) -> np.ndarr
 
 
 def q8_0_dequant(w: np.ndarray, ne0: int) -> np.ndarray:
-    """Q8_0 bytes [rows, ne0/32*34] -> f32 [rows, ne0] (d * qs)."""
+    """Q8_0 bytes [rows, ne0/32*34] -> f32 [rows, ne0] (d * qs): ggml's dequantize_row_q8_0
+    (vendor/llama.cpp/ggml/src/ggml-quants.c:553-567; the f32 product is exact)."""
     rows = w.shape[0]
     nb = ne0 // 32
     b = np.ascontiguousarray(w).reshape(rows, nb, 34)
     d = b[:, :, :2].copy().view(np.float16).astype(np.float32).reshape(rows, nb, 1)
     qs = b[:, :, 2:].copy().view(np.int8).astype(np.float32)
     return (d * qs).reshape(rows, ne0)
+
+
+def q8_0_quantize(x: np.ndarray, mutant: int = 0) -> np.ndarray:
+    """f32 rows [rows, ne0] -> Q8_0 bytes [rows, ne0/32*34]: ggml's reference quantiser
+    quantize_row_q8_0_ref (vendor/llama.cpp/ggml/src/ggml-quants.c:276-299), per 32-value block:
+    amax = max |x|, d = amax / 127 in f32, id = 1 / d in f32 (0 when d = 0), the stored scale
+    f16(d) (round to nearest even), q = roundf(x * id) with the product in f32 and roundf's half
+    away from zero.  (The 8-bit latent cache of the Q8_0 KQKV kernel is ggml's block_q8_0.)
+    Test mutants (never used by the library): 1 rounds half to even, 2 takes id from the stored f16
+    scale, 3 stores a scale one f16 ulp off the nearest."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, ne0 = x.shape
+    assert ne0 % 32 == 0
+    b = x.reshape(rows, ne0 // 32, 32)
+    amax = np.abs(b).max(axis=2)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    d16 = d.astype(np.float16)
+    dd = d16.astype(np.float32) if mutant == 2 else d
+    with np.errstate(divide="ignore"):
+        idv = np.where(dd != 0, np.float32(1.0) / dd, np.float32(0.0)).astype(np.float32)
+    x0 = (b * idv[:, :, None]).astype(np.float32).astype(np.float64)     # the f32 product, exact in f64
+    q = np.round(x0) if mutant == 1 else np.sign(x0) * np.floor(np.abs(x0) + 0.5)
+    out = np.empty((rows, ne0 // 32, 34), dtype=np.uint8)
+    if mutant == 3:
+        d16 = (d16.view(np.uint16) ^ np.uint16(1)).view(np.float16)
+    out[:, :, :2] = d16.view(np.uint8).reshape(rows, ne0 // 32, 2)
+    out[:, :, 2:] = q.astype(np.int8).view(np.uint8)
+    return out.reshape(rows, ne0 // 32 * 34)
+
+
+def q8_0_dequant_f16(w: np.ndarray, ne0: int) -> np.ndarray:
+    """Q8_0 bytes -> the f16 values the Q8_0 KQKV kernel computes with: f16(q * d), the product exact
+    in f32 and rounded once (= an f32 dequantisation followed by a conversion to f16)."""
+    return q8_0_dequant(w, ne0).astype(np.float16)
 
 
 def wkb_q8(w: np.ndarray, d_n: int, d_v: int, n_head: int, q_nope: np.ndarray, mutant: int = 0) -> np.ndarray:

@@ -219,3 +219,30 @@ def test_phase_entry_points_reject_before_launching():
     assert lib.mla_m4_phase_kvwrite(*(P(v) for v in descs), None, P(ops.view(torch.zeros(320))), None) == -1
     assert lib.mla_m4_phase_kvwrite(*(P(v) for v in descs), P(A.rope_params(n_dims=64, **RP)),
                                     P(ops.view(torch.zeros(300))), None) == -3
+
+
+# ------------------------------------------------------------------ 8-bit (Q8_0) latent cache
+def test_supports_kqkv_q8_cache():
+    """A Q8_0 cache (ggml block_q8_0 rows) at both instantiated geometries; other widths, a
+    non-block width and padded rows are refused.  Its partials hold f16 o, like an F16 cache's."""
+    _, q, mask, out = decode_tensors(n_kv=1000)
+    assert A.supports_kqkv(q8((1000,), 576), q, mask, out)
+    _, q3, mask3, out3 = decode_tensors(n_kv=1000, dk=320, dv=256, nt=3)
+    assert A.supports_kqkv(q8((1000,), 320), q3, mask3, out3)
+    _, q5, mask5, out5 = decode_tensors(n_kv=1000, dk=512, dv=448)
+    assert not A.supports_kqkv(q8((1000,), 512), q5, mask5, out5)                 # no Q8_0 kernel for 512
+    kc = q8((1000,), 576)
+    padded = ops.view(kc)
+    padded.nb[1] = 640                                                            # rows not contiguous
+    P = ctypes.byref
+    lib = A.load_library()
+    vq, vm, vo = ops.view(q), ops.view(mask), ops.view(out)
+    assert lib.mla_m4_supports_kqkv(P(ops.view(kc)), P(vq), P(vm), P(vo)) == 1
+    assert lib.mla_m4_supports_kqkv(P(padded), P(vq), P(vm), P(vo)) == 0
+    odd = ops.view(kc)
+    odd.ne[0] = 560                                                               # not whole 32-value blocks
+    assert lib.mla_m4_supports_kqkv(P(odd), P(vq), P(vm), P(vo)) == 0
+    S = A.default_splits(32768, 32, ops.TYPE_Q8_0)
+    assert S == 256
+    _, q, _, out = decode_tensors(n_kv=32768)
+    assert A.kqkv_workspace_bytes(q8((32768,), 576), q, out) == S * ops.part_floats(512, True) * 4

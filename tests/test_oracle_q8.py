@@ -277,3 +277,88 @@ def test_kvwrite_yarn_ramp(pos):
     for mutant in (3, 4):
         bad = orc.kvwrite(cur, w, d_lat, n_rope, nw, kc.copy(), 1, pos, rp, mutant=mutant)
         assert yarn_max_err(bad, gemv, d_lat, n_rope, pos, rp, list(range(n_rope // 2))) > 10 * tol, mutant
+
+
+# ---------------------------------------------------------------- the 8-bit (Q8_0) latent cache
+def q8_fields(wq, ne0):
+    b = np.ascontiguousarray(wq).reshape(wq.shape[0], ne0 // 32, 34)
+    d16 = b[:, :, :2].copy().view(np.float16).reshape(wq.shape[0], ne0 // 32)
+    qs = b[:, :, 2:].copy().view(np.int8).astype(np.int64)
+    return d16, qs
+
+
+def q8_checks(x, wq):
+    """Independent float64 checks of a Q8_0 quantisation of x: (stored scale is the f16 nearest to
+    amax / 127, every q is the integer nearest to x / d away from the ties, the max element maps to
+    +-127, zero blocks stay zero); returns a list of the failed checks."""
+    ne0 = x.shape[1]
+    d16, qs = q8_fields(wq, ne0)
+    b = x.astype(np.float64).reshape(x.shape[0], ne0 // 32, 32)
+    amax = np.abs(b).max(axis=2)
+    d = amax / 127.0
+    bad = []
+    # the f16 nearest to d: within half an f16 ulp (ulp from the f16 exponent of d)
+    ulp = np.where(d > 0, 2.0 ** (np.floor(np.log2(np.maximum(d, 2.0 ** -24))) - 10), 2.0 ** -24)
+    if not (np.abs(d16.astype(np.float64) - d) <= 0.5 * ulp * (1 + 1e-9)).all():
+        bad.append("scale")
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(d[:, :, None] > 0, b / d[:, :, None], 0.0)
+    away = np.sign(r) * np.floor(np.abs(r) + 0.5)
+    clear = np.abs(np.abs(r - np.trunc(r)) - 0.5) > 1e-4          # not near a tie
+    if not (qs[clear] == away[clear]).all():
+        bad.append("nearest")
+    if not (np.abs(qs).max(axis=2)[amax > 0] == 127).all() or (qs[amax == 0] != 0).any():
+        bad.append("ends")
+    return bad
+
+
+def test_q8_0_quantiser_known_answers_and_mutants():
+    """ggml's quantize_row_q8_0_ref (ggml-quants.c:276-299): d = amax / 127 stored as the nearest
+    f16, q = roundf(x * (1 / d)), half away from zero.  A block with amax = 127 has d = 1, so its q
+    are roundf(x) exactly: 62.5 -> 63, -62.5 -> -63, 0.5 -> 1, 2.5 -> 3."""
+    x = np.zeros((2, 32), np.float32)
+    x[0, :8] = [127, -127, 62.5, -62.5, 0.5, -0.5, 2.5, 1.4999999]
+    wq = orc.q8_0_quantize(x)
+    d16, qs = q8_fields(wq, 32)
+    assert d16[0, 0] == 1.0 and d16[1, 0] == 0.0
+    assert qs[0, 0, :8].tolist() == [127, -127, 63, -63, 1, -1, 3, 1]
+    assert (qs[1] == 0).all()
+    assert orc.q8_0_quantize(x, mutant=1).reshape(2, 34)[0, 2:10].view(np.int8).tolist() != qs[0, 0, :8].tolist()
+    # random rows of both cache widths: every independent check holds, and each mutant fails one
+    rng = np.random.default_rng(77)
+    for ne0 in (576, 320):
+        xr = (rng.standard_normal((64, ne0)) * rng.uniform(0.01, 3.0, (64, 1))).astype(np.float32)
+        xr[3, 32:64] = 0.0                                          # a zero block
+        assert q8_checks(xr, orc.q8_0_quantize(xr)) == []
+        assert "nearest" in q8_checks(xr, orc.q8_0_quantize(xr, mutant=2))    # id from the f16 scale
+        assert "scale" in q8_checks(xr, orc.q8_0_quantize(xr, mutant=3))      # scale off its nearest f16
+
+
+def test_q8_0_round_trip_and_f16_dequantisation():
+    """|x - q d16| <= d16 / 2 + 127 |d16 - d| per element; the f16 cache values of the Q8_0 kernel
+    are f16(q * d16) with the product exact (computed here in float64)."""
+    rng = np.random.default_rng(78)
+    x = (rng.standard_normal((100, 576)) * 0.7).astype(np.float32)
+    wq = orc.q8_0_quantize(x)
+    d16, qs = q8_fields(wq, 576)
+    d = np.abs(x.astype(np.float64)).reshape(100, 18, 32).max(axis=2) / 127.0
+    deq = orc.q8_0_dequant(wq, 576).astype(np.float64).reshape(100, 18, 32)
+    bound = d16.astype(np.float64) / 2 + 127 * np.abs(d16.astype(np.float64) - d) + 1e-12
+    assert (np.abs(x.astype(np.float64).reshape(100, 18, 32) - deq) <= bound[:, :, None]).all()
+    exact = (qs.astype(np.float64) * d16.astype(np.float64)[:, :, None]).reshape(100, 576)
+    assert np.array_equal(orc.q8_0_dequant_f16(wq, 576), exact.astype(np.float16))
+    assert np.array_equal(orc.q8_0_dequant(wq, 576).astype(np.float64), exact)
+
+
+def test_synthetic_q8_cache_matches_the_oracle_quantiser():
+    """aubier_amd.inputs builds the benchmark's Q8_0 caches with its own copy of the quantiser: it
+    must produce the oracle's bytes, and with_q8_cache's f16 values must be the oracle's f16(q d)."""
+    from aubier_amd import inputs as I
+    rng = np.random.default_rng(79)
+    x = (rng.standard_normal((300, 576)) * rng.uniform(0.001, 2.0, (300, 1))).astype(np.float32)
+    x[7, :64] = 0.0
+    x[8, 5] = 62.5 * (np.abs(x[8, :32]).max() / 127.0)       # a value near a rounding tie
+    assert np.array_equal(I.q8_0_rows(x), orc.q8_0_quantize(x))
+    inp = I.with_q8_cache(I.make_config(2, n_kv=300))
+    assert np.array_equal(inp.kcache_q8, orc.q8_0_quantize(I.make_config(2, n_kv=300).kcache.astype(np.float32)))
+    assert np.array_equal(inp.kcache, orc.q8_0_dequant_f16(inp.kcache_q8, 576))
