@@ -108,8 +108,9 @@ struct KvWriteArgs {
     const float * cur;
     const uint8_t * w;      // Q8_0 rows [d_lat + n_rope] of n_embd / 32 blocks
     const float * nw;       // [d_lat]
-    void * kcache;          // F16 rows of kc_nb1 bytes
+    void * kcache;          // F16 rows of kc_nb1 bytes, or Q8_0 rows (kc_q8) of 34-byte blocks
     int64_t kc_nb1;
+    int kc_q8;
     int64_t n_kv;
     const int64_t * kidx;
     const int32_t * pos;

@@ -263,7 +263,8 @@ int check_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * w, const mla_
         !has_data(kidx, plan) || !has_data(pos, plan) || !has_data(dst, plan) || !rp)
         return MLA_M4_ERR_NULL;
     if (cur->type != MLA_M4_TYPE_F32 || w->type != MLA_M4_TYPE_Q8_0 || nw->type != MLA_M4_TYPE_F32 ||
-        kc->type != MLA_M4_TYPE_F16 || kidx->type != MLA_M4_TYPE_I64 || pos->type != MLA_M4_TYPE_I32 ||
+        (kc->type != MLA_M4_TYPE_F16 && kc->type != MLA_M4_TYPE_Q8_0) || kidx->type != MLA_M4_TYPE_I64 ||
+        pos->type != MLA_M4_TYPE_I32 ||
         dst->type != MLA_M4_TYPE_F32)
         return MLA_M4_ERR_TYPE;
     const int64_t n_embd = cur->ne[0], n_out = w->ne[1], n_dims = rp->n_dims, d_lat = n_out - n_dims;
@@ -277,7 +278,14 @@ int check_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * w, const mla_
     if (!is_contiguous(cur) || !is_contiguous(nw) || !is_contiguous(dst) || !al4(cur->data, plan) ||
         !al4(nw->data, plan) || !al4(dst->data, plan))
         return MLA_M4_ERR_STRIDE;
-    if (kc->nb[0] != 2 || kc->nb[1] < (size_t)n_out * 2 || (kc->nb[1] & 1u)) return MLA_M4_ERR_STRIDE;
+    if (kc->type == MLA_M4_TYPE_F16) {
+        if (kc->nb[0] != 2 || kc->nb[1] < (size_t)n_out * 2 || (kc->nb[1] & 1u)) return MLA_M4_ERR_STRIDE;
+    } else {
+        // Q8_0 rows: whole blocks (n_out is a multiple of 32, checked below), 2-byte aligned scales
+        if (n_out % 32 || kc->nb[0] != 34 || kc->nb[1] < (size_t)(n_out / 32) * 34 || (kc->nb[1] & 1u) ||
+            (reinterpret_cast<uintptr_t>(kc->data) & 1u))
+            return MLA_M4_ERR_STRIDE;
+    }
     if (!(rp->freq_base > 0.0f) || !(rp->freq_scale > 0.0f) || !(rp->eps >= 0.0f) || rp->n_ctx_orig < 1 ||
         !std::isfinite(rp->ext_factor) || !std::isfinite(rp->attn_factor) || !(rp->beta_fast > 0.0f) ||
         !(rp->beta_slow > 0.0f))
@@ -512,6 +520,7 @@ int mla_m4_phase_kvwrite(const mla_m4_tensor * cur, const mla_m4_tensor * wkv_a,
     a.nw = static_cast<const float *>(kv_norm->data);
     a.kcache = kcache->data;
     a.kc_nb1 = (int64_t)kcache->nb[1];
+    a.kc_q8 = kcache->type == MLA_M4_TYPE_Q8_0;
     a.n_kv = kcache->ne[1];
     a.kidx = static_cast<const int64_t *>(kidx->data);
     a.pos = static_cast<const int32_t *>(pos->data);

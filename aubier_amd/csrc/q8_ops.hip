@@ -2,7 +2,7 @@
 //   * GGML_OP_M4_WKB with a Q8_0 W_kb (patches/ggml-m4/m4-wkb.cu:14-86),
 //   * GGML_OP_M4_PHASE phase 1, wv_b (m4-phase.cu:44-89, 209-224),
 //   * GGML_OP_M4_PHASE phase 0, KV-write: wkv_a gemv, RMS norm, YaRN rope and the in-place f16
-//     scatter into the cache (m4-phase.cu:91-200, 226-273).
+//     (or Q8_0) scatter into the cache (m4-phase.cu:91-200, 226-273).
 // Numerics are the reference kernels' (the GPU MMVQ form, not ggml-cpu's): the f32 activation is
 // quantised per 32-value block (d = amax / 127, an f16 scale, int8 quants by roundf(x / d) in
 // WKB and roundf(x * (1 / d)) in the PHASE ops), block dots are exact int32 sums (v_dot4_i32_i8),
@@ -183,7 +183,11 @@ __global__ __launch_bounds__(NBE) void kvwrite_gemv_kernel(KvWriteArgs a) {
 // rows are reduced (butterfly per 32 rows, then the partials in order), and each thread writes its
 // final value to dst and, as f16, to cache row kidx -- read on the device from the graph's
 // tensors; a row outside [0, n_kv) is not written (the reference trusts the engine; this
-// implementation refuses to scatter out of bounds).
+// implementation refuses to scatter out of bounds).  With a Q8_0 cache (kc_q8) each 32-thread
+// half-wavefront holds one block of the row and stores it as ggml's f32 -> q8_0 copy does
+// (quantize_row_q8_0_ref, ggml-quants.c:276-299): d = amax / 127, q = roundf(x * (1 / d)), the
+// f16 scale by the block's first lane, one int8 per lane.  n_out is a multiple of 32, so a
+// half-wavefront is either all inside the row or all past it.
 __global__ __launch_bounds__(1024) void kvwrite_tail_kernel(KvWriteArgs a) {
     __shared__ float sred[32];
     const int tid = threadIdx.x;
@@ -221,6 +225,19 @@ __global__ __launch_bounds__(1024) void kvwrite_tail_kernel(KvWriteArgs a) {
         }
         const float co = cosf(theta) * mscale, si = sinf(theta) * mscale;
         out = ((tid - a.d_lat) & 1) ? x0 * si + x1 * co : x0 * co - x1 * si;
+    }
+    if (a.kc_q8) {
+        float d16;
+        const int q = quant_lane<false>(out, d16);   // every lane takes part in the block max
+        if (tid < n_out) {
+            a.dst[tid] = out;
+            if (row >= 0 && row < a.n_kv) {
+                char * blk = reinterpret_cast<char *>(a.kcache) + (size_t)row * a.kc_nb1 + (size_t)(tid >> 5) * 34;
+                if ((tid & 31) == 0) *reinterpret_cast<half_t *>(blk) = (half_t)d16;
+                reinterpret_cast<int8_t *>(blk + 2)[tid & 31] = (int8_t)q;
+            }
+        }
+        return;
     }
     if (tid < n_out) {
         a.dst[tid] = out;

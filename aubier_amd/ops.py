@@ -373,8 +373,9 @@ def ggml_m4_phase_kvwrite(cur: torch.Tensor, wkv_a: Q8_0, kv_norm: torch.Tensor,
                           kidx: torch.Tensor, pos: torch.Tensor, rope: RopeParams,
                           out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """GGML_OP_M4_PHASE phase 0 (KV-write): cur f32 [n_embd]; wkv_a Q8_0 blocks [n_out, n_embd/32*34];
-    kv_norm f32 [d_lat]; kcache f16 [n_kv, n_out] (row kidx[0] written in place); kidx int64 [1];
-    pos int32 [1] -> Kcur f32 [n_out]."""
+    kv_norm f32 [d_lat]; kcache f16 [n_kv, n_out] or Q8_0 (rows of n_out / 32 blocks; row kidx[0]
+    written in place, quantised as ggml's f32 -> q8_0 copy); kidx int64 [1]; pos int32 [1] -> Kcur
+    f32 [n_out]."""
     lib = load_library()
     if out is None:
         out = torch.empty((wkv_a.blocks.shape[0],), dtype=torch.float32, device=cur.device)

@@ -220,6 +220,10 @@ typedef struct mla_m4_rope_params {
  *   wkv_a   Q8_0 ne [n_embd, d_lat + n_dims]  rows of n_embd / 32 blocks
  *   kv_norm F32  ne [d_lat]                   attn_kv_a_norm weight
  *   kcache  F16  ne [d_lat + n_dims, n_kv]    WRITTEN IN PLACE at row kidx[0] (as ggml_set_rows)
+ *           or Q8_0 (an extension: the reference's cache is F16 only; rows of (d_lat + n_dims) / 32
+ *           blocks, nb[0] = 34, nb[1] even) -- the row is quantised as ggml's f32 -> q8_0 copy
+ *           does (quantize_row_q8_0_ref, ggml-quants.c:276-299: per 32 values d = amax / 127,
+ *           q = roundf(x * (1 / d)), d stored as f16), the cache KQKV reads as an 8-bit cache
  *   kidx    I64  ne [1], pos I32 ne [1]       read on the device (no host read of device memory);
  *                                             a row outside [0, n_kv) is not written
  *   dst     F32  ne [d_lat + n_dims]          Kcur: the values the cache row received

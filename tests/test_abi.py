@@ -210,6 +210,27 @@ def test_supports_phase_kvwrite():
     assert not A.supports_phase_kvwrite(*kv_descs(), bad, torch.zeros(320))
 
 
+def test_supports_phase_kvwrite_q8_cache():
+    """KV-write into an 8-bit (Q8_0) cache: whole-block rows, 2-byte aligned scales."""
+    rp = A.rope_params(n_dims=64, **RP)
+    lib = A.load_library()
+    for n_embd, d_lat in ((4096, 256), (7168, 512)):
+        d = list(kv_descs(n_embd, d_lat))
+        n_out = d_lat + 64
+        d[3] = q8((100,), n_out)
+        assert A.supports_phase_kvwrite(*d, rp, torch.zeros(n_out))
+        v = [ops.view(t) for t in d]
+        dst = ops.view(torch.zeros(n_out))
+        ok = lambda: lib.mla_m4_supports_phase_kvwrite(*(ctypes.byref(x) for x in v), ctypes.byref(rp), ctypes.byref(dst))
+        v[3].nb[1] += 2                                     # padded rows: fine
+        assert ok()
+        v[3].nb[1] += 1                                     # odd row pitch: scales unaligned
+        assert not ok()
+        v[3].nb[1] -= 3
+        v[3].nb[0] = 32                                     # not ggml's block size
+        assert not ok()
+
+
 def test_phase_entry_points_reject_before_launching():
     lib = A.load_library()
     P = ctypes.byref

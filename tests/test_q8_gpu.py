@@ -8,7 +8,10 @@ bit-identical to the oracle.  KV-write's gemv is bit-identical too (seen directl
 at pos = 0, where the rotation is the identity); the RMS norm uses the hardware rsqrt (the
 reference's rsqrtf; the oracle divides by sqrtf): <= 4 ulp; the rope rows use the device's powf /
 sinf / cosf (the oracle the C library's): |err| <= 1e-6 + 4e-7 pos max|x|, the f32 resolution of
-an angle of size pos.  The cache row must equal f16(dst) and be the only row written.
+an angle of size pos.  The cache row must equal f16(dst) and be the only row written.  With an
+8-bit (Q8_0) cache -- an extension, the reference's cache is f16 -- the row must hold exactly
+ggml's quantize_row_q8_0_ref of dst (oracle.q8_0_quantize, pinned in test_oracle_q8.py), and dst
+must be the f16-cache launch's, bit for bit.
 """
 import numpy as np
 import pytest
@@ -118,3 +121,60 @@ def test_kvwrite_row_outside_cache_is_not_written(dev):
         torch.cuda.synchronize()
         assert np.isfinite(out.cpu().numpy()).all()
     assert np.array_equal(kc_d.cpu().numpy().view(np.uint16), kc0.view(np.uint16))
+
+
+@pytest.mark.parametrize("n_embd,d_lat,pos,yarn", [(4096, 256, 77, False), (7168, 512, 5000, True)])
+def test_kvwrite_q8_cache(dev, n_embd, d_lat, pos, yarn):
+    """KV-write into a Q8_0 cache, then KQKV reads the row back: the stored blocks are the oracle's
+    quantisation of the launch's own Kcur, every other row is untouched, and KQKV over the cache
+    sees f16(q * d) of that row."""
+    n_rope, n_kv, row = 64, 300, 123
+    n_out = d_lat + n_rope
+    rng = np.random.default_rng(8500 + d_lat)
+    w = orc.q8_0_random(8501, n_out, n_embd, scale=0.002)
+    cur = rng.standard_normal(n_embd).astype(np.float32)
+    nw = (1.0 + 0.25 * rng.standard_normal(d_lat)).astype(np.float32)
+    kc0 = orc.q8_0_quantize(rng.standard_normal((n_kv, n_out)).astype(np.float32))
+    rp = A.rope_params(n_dims=n_rope, **(RP_YARN if yarn else RP_PLAIN))
+    args = (torch.from_numpy(cur).to(dev), q8_dev(w, (n_out,), n_embd, dev), torch.from_numpy(nw).to(dev))
+    kidx, pos_d = torch.tensor([row], dtype=torch.int64, device=dev), torch.tensor([pos], dtype=torch.int32, device=dev)
+    kc_q = torch.from_numpy(kc0.copy()).to(dev)
+    out = A.ggml_m4_phase_kvwrite(*args, A.Q8_0(kc_q, n_out), kidx, pos_d, rp)
+    kc_h = torch.zeros((n_kv, n_out), dtype=torch.float16, device=dev)
+    out_h = A.ggml_m4_phase_kvwrite(*args, kc_h, kidx, pos_d, rp)
+    torch.cuda.synchronize()
+    got, kc = out.cpu().numpy(), kc_q.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), out_h.cpu().numpy().view(np.uint32))
+    want = orc.q8_0_quantize(got[None, :])[0]
+    say(f"KV-write Q8_0 {n_embd}->{d_lat}+{n_rope} pos={pos}: {np.count_nonzero(kc[row] != want)} bytes differ")
+    assert np.array_equal(kc[row], want)
+    others = np.ones(n_kv, bool)
+    others[row] = False
+    assert np.array_equal(kc[others], kc0[others])
+    # the row as KQKV reads it: one head whose q picks out column j of the cache (a one-key window)
+    deq = orc.q8_0_dequant_f16(kc[row:row + 1], n_out)[0]
+    assert np.abs(deq.astype(np.float32) - got).max() <= np.abs(got).max() * (0.5 / 127.0 + 2.0 ** -11) * 1.01
+    mask = np.full((1, n_kv), -np.inf, dtype=np.float32)
+    mask[0, row] = 0.0
+    q = np.zeros((1, 32, n_out), dtype=np.float32)
+    o = A.ggml_m4_kqkv(A.Q8_0(kc_q, n_out), torch.from_numpy(q).to(dev), torch.from_numpy(mask).to(dev), 1.0)
+    torch.cuda.synchronize()
+    # with one key unmasked its softmax weight is 1: out = its first d_lat values
+    np.testing.assert_allclose(o.cpu().numpy()[0, 0], deq[:d_lat].astype(np.float32), rtol=1e-6, atol=0)
+
+
+def test_kvwrite_q8_row_outside_cache_is_not_written(dev):
+    n_embd, d_lat, n_rope, n_kv = 4096, 256, 64, 16
+    n_out = d_lat + n_rope
+    w = orc.q8_0_random(8600, n_out, n_embd, scale=0.002)
+    cur = np.random.default_rng(8601).standard_normal(n_embd).astype(np.float32)
+    kc0 = orc.q8_0_quantize(np.random.default_rng(8602).standard_normal((n_kv, n_out)).astype(np.float32))
+    kc_q = torch.from_numpy(kc0.copy()).to(dev)
+    args = (torch.from_numpy(cur).to(dev), q8_dev(w, (n_out,), n_embd, dev),
+            torch.ones(d_lat, dtype=torch.float32, device=dev), A.Q8_0(kc_q, n_out))
+    for bad in (n_kv, n_kv + 5, -1):
+        out = A.ggml_m4_phase_kvwrite(*args, torch.tensor([bad], dtype=torch.int64, device=dev),
+                                      torch.tensor([3], dtype=torch.int32, device=dev), A.rope_params(n_dims=n_rope, **RP_PLAIN))
+        torch.cuda.synchronize()
+        assert np.isfinite(out.cpu().numpy()).all()
+    assert np.array_equal(kc_q.cpu().numpy(), kc0)
