@@ -14,7 +14,8 @@
 //     unlike the f16 kernel, the q staging does not share LDS with the stream;
 //   * per tile: barrier (every wave is past the previous tile's P.V) -> each wave dequantises its
 //     slice into the f16 tile -> it issues the DMA of tile k + 2 into the slot it has just read ->
-//     barrier -> the f16 kernel's Q.K^T of its slice, scores, lazy reference max and P.V;
+//     the f16 kernel's Q.K^T of its own slice, scores, the maxima exchange (a barrier, after which
+//     the whole f16 tile is in place), lazy reference max and P.V;
 //   * dequantisation: f16(q * d), the value a conversion of the dequantised f32 to f16 gives (the
 //     product q * d is exact in f32, so both round once): each int8 enters f16 exactly as
 //     (1024 + (q + 128)) - 1152 (the byte biased by 128 under the f16 bit pattern of 1024, then
@@ -182,7 +183,9 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_q8_kernel(DecodeArgs a) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             q8_dma<DK>(ss, ring8, s, k + 2, lane);
         }
-        __syncthreads();                     // the f16 tile is complete
+        // no barrier here: Q.K^T reads only this wave's own slice (its LDS accesses are in order),
+        // and P.V, which reads every slice, follows the maxima barrier below, which every wave
+        // reaches after its dequantisation
 
         f32x4 s0, s1;
         qk_slice<DK, false, false>(ss, SliceDma{}, sb, lane, qreg, s0, s1);

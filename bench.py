@@ -475,7 +475,7 @@ def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = F
     us = time_fn(step, reps)
 
     part = None
-    n_split = max(1, need // (((H + 31) // 32) * T * A.ops.part_floats(DV) * 4)) if need else 1
+    n_split = max(1, need // (((H + 31) // 32) * T * A.ops.part_floats(DV, inp.kc_f16) * 4)) if need else 1
     if n_split > 1:
         part = torch.empty(((H + 31) // 32, T, n_split, A.ops.part_floats(DV, inp.kc_f16)), dtype=torch.float32, device=dev)
     # per kernel: 12 replays of a 4-launch graph (fewer read low right after another config's run)
