@@ -118,6 +118,22 @@ def test_q8_cache_cases(dev, dk, dv, n_kv, nt, splits, holes, q_scale):
         assert eq <= bound
 
 
+def test_q8_cache_chunked_prefill(dev):
+    """A chunk of 20 tokens over a Q8_0 cache with a causal mask (token i sees the cached keys and
+    new keys up to its own): the 8-bit kernel runs one workgroup per token (no token batching, so
+    prefill over an 8-bit cache is correct but not the MFMA prefill kernel's speed)."""
+    n_kv, nt, dk, dv, H = 1500, 20, 576, 512, 32
+    kc = I.randn(7400, n_kv * dk).astype(np.float16).reshape(n_kv, dk)
+    q = I.randn(7401, nt * H * dk, 0.05).reshape(nt, H, dk)
+    mask = np.zeros((nt, n_kv), dtype=np.float32)
+    for t in range(nt):
+        mask[t, n_kv - nt + t + 1:] = -np.inf
+    _, deq, kq = q8_cache(kc, dev)
+    ref = orc.kqkv(deq, q, mask, SCALE, d_v=dv)
+    out = run(kq, torch.from_numpy(q).to(dev), torch.from_numpy(mask).to(dev), None, dv)
+    check("q8 chunked prefill nt=20 vs oracle(dequantised)", out, ref, 1e-2, 3e-3)
+
+
 def test_q8_cache_noalloc_matches(dev):
     """The no-allocation entry point runs the same Q8_0 kernels: bit-exact with ggml_m4_kqkv."""
     n_kv, dk = 32768, 576
