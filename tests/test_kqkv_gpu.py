@@ -95,9 +95,10 @@ def test_partials_match_oracle(dev):
     m, l, o = A.ops.decode_partials(part, I.N_HEAD)
     ref = orc.partials(inp.kcache, qcur, inp.mask, inp.kq_scale, orc.split_bounds(inp.n_kv, S))
     # A block's (m, l) is one representation of the split's log-sum-exp: the decode kernel's m is
-    # its shared reference maximum, at most 8 ln 2 below the split's max, with l relative to it.
-    # The merge depends on m + ln l only; that, the bound on m and o/l are what is checked.
-    assert np.all(m <= ref[..., 0] + 2e-3) and np.all(m >= ref[..., 0] - 8 * np.log(2) - 2e-3)
+    # its shared reference maximum, at most 15 ln 2 below the split's max (the lazy move bound: P =
+    # 2^(s - m) <= 2^15), with l relative to it.  The merge depends on m + ln l only; that, the
+    # bound on m and o/l are what is checked.
+    assert np.all(m <= ref[..., 0] + 2e-3) and np.all(m >= ref[..., 0] - 15 * np.log(2) - 2e-3)
     assert np.allclose(m + np.log(l), ref[..., 0] + np.log(ref[..., 1]), atol=2e-3)
     check("partials o/l", o, ref[..., 4:] / ref[..., 1:2], True)
 
