@@ -132,6 +132,19 @@ bool use_q8(const KqkvShape & s) { return s.kc_type == MLA_M4_TYPE_Q8_0; }
 
 int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
 
+// Single-token decode over an f16 cache (one 32-head group): the step is the partial and then the
+// merge, which reads every split's record (32 heads x D_v f16) back cold, straight after the
+// partial wrote it, so fewer and longer splits can win although the partial alone slows.  From
+// measured steps on the MI355X (WKB + partial + merge, COLD): one tile per split up to 160 tiles,
+// two up to 384, 192 splits up to 768 tiles (32,768 keys: 19.95 us against 20.7-21.2 at 256),
+// then 256.
+int64_t decode_f16_step_splits(int64_t tiles) {
+    if (tiles <= 160) return tiles;
+    if (tiles <= 384) return (tiles + 1) / 2;
+    if (tiles <= 768) return 192;
+    return TARGET_WG;
+}
+
 int default_splits(const KqkvShape & s) {
     // the unit a split is made of: 64-key tiles (MFMA kernels), 16-key granules (VALU kernel)
     const int64_t tiles = (use_mfma(s) || use_q8(s)) ? n_tiles_of(s.n_kv) : (s.n_kv + mla::GRAN_KEYS - 1) / mla::GRAN_KEYS;
@@ -145,6 +158,7 @@ int default_splits(const KqkvShape & s) {
     else if (use_q8(s)) groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) * s.nt;
     else groups = s.n_head * s.nt;
     int64_t sp = (TARGET_WG + groups - 1) / groups;
+    if (use_mfma(s) && !use_prefill(s) && s.nt == 1 && groups == 1) sp = decode_f16_step_splits(tiles);
     if (sp > tiles) sp = tiles;
     if (sp > MLA_M4_MAX_SPLITS) sp = MLA_M4_MAX_SPLITS;
     if (sp < 1) sp = 1;

@@ -124,7 +124,12 @@ def test_supports_phase():
 
 
 def test_default_splits_and_workspace(lib):
-    assert A.default_splits(32768) == 256
+    # one token, f16 cache: chosen for the partial + merge step (1 tile per split up to 160 tiles,
+    # 2 up to 384, 192 splits up to 768 tiles, 256 beyond)
+    assert A.default_splits(32768) == 192
+    assert A.default_splits(8192) == 128 and A.default_splits(16384) == 128 and A.default_splits(24576) == 192
+    assert A.default_splits(65536) == 256 and A.default_splits(262144) == 256
+    assert A.default_splits(32768, 32, ops.TYPE_Q8_0) == 256                # the 8-bit cache keeps 256
     assert A.default_splits(64) == 1
     assert 1 <= A.default_splits(4096) <= 64                     # at most one split per 64-key tile
     assert A.default_splits(262144) <= ops.MAX_SPLITS
