@@ -239,12 +239,17 @@ class Decode:
         return self.time_graph(self.capture(lambda i: self.step(0), self.glen), reps, self.glen)
 
     def split_sweep(self, reps):
+        """Per split count: the partial and the merge each in graphs of their own launches, and the
+        whole step (WKB -> partial -> merge), in which the merge reads the records the partial has
+        just written."""
         res = {}
         for S in (64, 128, 192, 256):
             p = self.new_part(S)
             ua = self.time_graph(self.capture(lambda i, p=p, S=S: self.attn(i, p, S), self.glen), reps, self.glen)
             um = self.time_graph(self.capture(lambda i, p=p: self.merge(p), self.glen), reps, self.glen)
-            res[str(S)] = {"us_partial": round(ua, 3), "us_merge": round(um, 3),
+            us = self.time_graph(self.capture(lambda i, p=p, S=S: (self.wkb(i), self.attn(i, p, S), self.merge(p)), self.glen),
+                                 reps, self.glen)
+            res[str(S)] = {"us_partial": round(ua, 3), "us_merge": round(um, 3), "us_step": round(us, 3),
                            "partial_GBps": round(self.bytes_attn / (ua * 1e3), 1)}
         return res
 
