@@ -1,6 +1,6 @@
-// decode_common.h -- the parts shared by the two split-K decode kernels (kqkv_decode.hip for
-// splits of a few tiles, kqkv_decode_long.hip for long splits): the KV slice geometry and its LDS
-// slot layout, the slice DMA, the q staging prologue and the Q.K^T step.
+// decode_common.h -- the parts shared by the split-K kernels over an f16 cache (kqkv_decode.hip,
+// and in part the prefill and 8-bit cache kernels): the KV slice geometry and its LDS slot layout,
+// the slice DMA, the q staging prologue, the Q.K^T step, P.V and the end of a split.
 //
 // A split is a run of whole 64-key tiles; wave w of the workgroup owns keys 16 w .. 16 w + 15 of
 // every tile (its "slice") and streams them into its own slot of a two-stage LDS ring by bounds-
@@ -143,7 +143,7 @@ struct SliceStream {
     }
 };
 
-constexpr int SHORT_MAX_TILES = 6;   // longest split of the barrier-per-tile kernel
+constexpr int LIVE_ROUND_TILES = 6;  // tiles per round trip of the row-liveness check
 constexpr int ROWS_MAX = 16;         // rows (tokens) per workgroup of the decode kernels
 
 // Workgroups along the row axis of a decode launch: rows t = z, z + Z, ... share a workgroup, Z as
@@ -159,8 +159,9 @@ inline int decode_row_groups(const DecodeArgs & a, int n_hgroups) {
 }
 
 // Liveness of this workgroup's rows in split sp: bit i set when row blockIdx.z + i gridDim.z has a
-// key with mask > -inf below n_kv in the split (splits of at most MAXT tiles).  Wave w checks rows
-// w, w + 4, w + 8, w + 12; every load is issued before the first compare (one round trip).
+// key with mask > -inf below n_kv in the split.  Wave w checks rows w, w + 4, w + 8, w + 12, MAXT
+// tiles of the split per round trip (every load of a round issued before its first compare), until
+// the split ends or every row it checks has been found live.
 template <int MAXT>
 __device__ __forceinline__ uint32_t live_rows_of_wave(const DecodeArgs & a, int sp, int w, int lane) {
     constexpr int RW = ROWS_MAX / NWAVE;
@@ -168,25 +169,31 @@ __device__ __forceinline__ uint32_t live_rows_of_wave(const DecodeArgs & a, int 
     const int t0 = sp * base_t + min(sp, rem);
     const int n_my = base_t + (sp < rem ? 1 : 0);
     const int k0 = t0 * TK, k1 = min((t0 + n_my) * TK, a.n_kv);
-    float v[RW][MAXT];
+    uint32_t rows = 0;                       // the rows this wave checks
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const int t = (int)blockIdx.z + (w + NWAVE * r) * (int)gridDim.z;
-        const float * row = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) +
-                                                            (size_t)min(t, a.nt - 1) * a.mask_nb1);
-#pragma unroll
-        for (int j = 0; j < MAXT; ++j) {
-            const int k = k0 + lane + 64 * j;
-            v[r][j] = (t < a.nt && k < k1) ? row[k] : -INFINITY;
-        }
-    }
+    for (int r = 0; r < RW; ++r)
+        if ((int)blockIdx.z + (w + NWAVE * r) * (int)gridDim.z < a.nt) rows |= 1u << (w + NWAVE * r);
     uint32_t bits = 0;
+    for (int kb = k0; kb < k1 && bits != rows; kb += TK * MAXT) {
+        float v[RW][MAXT];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        bool live = false;
+        for (int r = 0; r < RW; ++r) {
+            const int t = (int)blockIdx.z + (w + NWAVE * r) * (int)gridDim.z;
+            const float * row = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.mask) +
+                                                                (size_t)min(t, a.nt - 1) * a.mask_nb1);
 #pragma unroll
-        for (int j = 0; j < MAXT; ++j) live |= v[r][j] != -INFINITY;
-        if (__builtin_amdgcn_ballot_w64(live) != 0) bits |= 1u << (w + NWAVE * r);
+            for (int j = 0; j < MAXT; ++j) {
+                const int k = kb + lane + 64 * j;
+                v[r][j] = (t < a.nt && k < k1) ? row[k] : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            bool live = false;
+#pragma unroll
+            for (int j = 0; j < MAXT; ++j) live |= v[r][j] != -INFINITY;
+            if (__builtin_amdgcn_ballot_w64(live) != 0) bits |= 1u << (w + NWAVE * r);
+        }
     }
     return bits;
 }
@@ -311,14 +318,12 @@ __device__ __forceinline__ void vacc_settle(f32x4 & acc0, f32x4 & acc1, f32x4 & 
 // slice is DMA_N blocks then the mask, step s reading blocks 2 (s >> 1) and 2 (s >> 1) + 1; before
 // that read, the blocks after them, the mask and the next slice's instructions issued so far (one
 // per completed step) may still be in flight.
-// With DMA, the next slice's DMA (dn) is spread over the steps.  Operand reads run QPF steps ahead
-// of their MFMAs; the scheduling barriers keep the compiler from sinking them back next to their
-// use.  Two accumulator chains per head tile (even / odd steps) keep consecutive MFMAs
-// independent.  Returns with the slice's mask slot landed.  WAIT = false: the slice is known to
-// be in LDS already (no DMA accounting, no next-slice DMA).  NT: the cache policy of the next
-// slice's DMA (streaming for decode; cached where other workgroups re-read the cache).  VACC: the
-// accumulators in VGPRs (mfma16).
-template <int DK, bool DMA, bool WAIT = true, bool NT = true, bool VACC = false>
+// With DMA, the next slice's DMA (dn, streaming cache policy) is spread over the steps.  Operand
+// reads run QPF steps ahead of their MFMAs; the scheduling barriers keep the compiler from sinking
+// them back next to their use.  Two accumulator chains per head tile (even / odd steps) keep
+// consecutive MFMAs independent.  Returns with the slice's mask slot landed.  WAIT = false: the
+// slice is known to be in LDS already (no DMA accounting, no next-slice DMA).
+template <int DK, bool DMA, bool WAIT = true>
 __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const SliceDma & dn, const char * sb, int lane,
                                          const half8 (&qreg)[2][SliceGeom<DK>::QSTEPS], f32x4 & s0, f32x4 & s1) {
     static_assert(WAIT || !DMA, "a slice already in LDS comes with no DMA to spread");
@@ -345,22 +350,21 @@ __device__ __forceinline__ void qk_slice(const SliceStream<DK> & ss, const Slice
             abuf[s % QPF] = *arow(s + QPF);
         }
         if (s & 1) {
-            mfma16<VACC>(acc2, av, qreg[0][s], s == 1);
-            mfma16<VACC>(acc3, av, qreg[1][s], s == 1);
+            mfma16<false>(acc2, av, qreg[0][s], s == 1);
+            mfma16<false>(acc3, av, qreg[1][s], s == 1);
         } else {
-            mfma16<VACC>(acc0, av, qreg[0][s], s == 0);
-            mfma16<VACC>(acc1, av, qreg[1][s], s == 0);
+            mfma16<false>(acc0, av, qreg[0][s], s == 0);
+            mfma16<false>(acc1, av, qreg[1][s], s == 0);
         }
-        if constexpr (DMA) ss.template put<NT>(dn, s);
+        if constexpr (DMA) ss.put(dn, s);
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (DMA) {
-        ss.template put<NT>(dn, G::DMA_N);
+        ss.put(dn, G::DMA_N);
         wait_vm<G::DMA_N + 1>();             // the mask slot (the next slice's DMA_N + 1 may be in flight)
     } else if constexpr (WAIT) {
         wait_vm<0>();
     }
-    if constexpr (VACC) vacc_settle(acc0, acc1, acc2, acc3);
     s0 = acc0 + acc2;
     s1 = acc1 + acc3;
 }
@@ -443,8 +447,8 @@ __device__ __forceinline__ void slice_scores(const DecodeArgs & a, const f32x4 &
 // reference moves.
 __device__ __forceinline__ bool ref_moves(float m, float x) { return x > m + LAZY; }
 
-// ---------------------------------------------------------------- the short-split kernels
-// (kqkv_decode.hip: the plain pass-1 kernel and the one with the WKB prologue)
+// ---------------------------------------------------------------- the decode kernels
+// (kqkv_decode.hip, and the 8-bit cache kernel of kqkv_decode_q8.hip)
 
 // byte offset of wave slot v of ring stage s
 template <int DK>

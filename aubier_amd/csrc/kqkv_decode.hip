@@ -1,5 +1,6 @@
 // kqkv_decode.hip -- split-K MLA decode attention over an f16 latent+rope KV cache, on MFMA, for
-// splits of a few 64-key tiles (the 32K-key decode step: two tiles per workgroup).
+// splits of any number of 64-key tiles (the 32K-key decode step: two or three tiles per workgroup;
+// 262,144 keys: sixteen).
 //
 // The pass-1 kernel of GGML_OP_M4_KQKV (reference: patches/ggml-m4/m4-kqkv.cu:201-312), designed
 // for gfx950 rather than translated:
@@ -173,7 +174,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint32_t live = ~0u;
     if (a.nt > 1 && a.dst == nullptr && a.mask != nullptr) {
-        const uint32_t bits = live_rows_of_wave<SHORT_MAX_TILES>(a, blockIdx.x, w, lane);
+        const uint32_t bits = live_rows_of_wave<LIVE_ROUND_TILES>(a, blockIdx.x, w, lane);
         if (lane == 0) live_w[w] = bits;
         __syncthreads();
         live = live_w[0] | live_w[1] | live_w[2] | live_w[3];
@@ -201,14 +202,7 @@ static hipError_t launch_short(const DecodeArgs & a, int n_hgroups, hipStream_t 
     return hipGetLastError();
 }
 
-hipError_t launch_kqkv_decode_f16_long(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
-
-// Splits of at most SHORT_MAX_TILES tiles take the barrier-per-tile kernel above (short tail);
-// longer ones the independent-wave kernel of kqkv_decode_long.hip (no barrier in the loop,
-// costlier end).
 hipError_t launch_kqkv_decode_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream) {
-    const int tiles_per_split = (a.n_tiles + a.n_split - 1) / a.n_split;
-    if (tiles_per_split > SHORT_MAX_TILES) return launch_kqkv_decode_f16_long(dk, dv, a, stream);
     const int n_hgroups = (a.n_head + decode::HG - 1) / decode::HG;
     if (dk == 576 && dv == 512) return launch_short<576, 512>(a, n_hgroups, stream);
     if (dk == 320 && dv == 256) return launch_short<320, 256>(a, n_hgroups, stream);

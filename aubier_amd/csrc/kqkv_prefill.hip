@@ -121,7 +121,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
         }
     }
 
-    // ---- per-wave state (as in kqkv_decode_long.hip) ----
+    // ---- per-wave state ----
     float m_run[2] = {M_NONE, M_NONE};       // heads 16 n + j16, log2 units
     float l_acc = 0.0f;                      // head lane & 31, keys 8 (lane >> 5) .. +7 of each slice
     f32x16 o[C::NB];                         // o^T tile i: C row = column 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3), C col = head lane & 31
@@ -203,7 +203,9 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_prefill_f16_kernel(DecodeArgs a)
                     }
                 asm volatile("s_nop 7" ::: "memory");
             }
-            // P^T operand (two v_permlane16_swap; see kqkv_decode_long.hip)
+            // P^T operand: Q.K^T's C layout (lane: keys 4 g .. +3 of heads j16 and 16 + j16) into
+            // P.V's B layout (lane: keys 8 (lane >> 5) .. +7 of head lane & 31), one
+            // v_permlane16_swap per pair of f16 values
             uint32_t px[2], py[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {

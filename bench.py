@@ -42,20 +42,18 @@ COLD_BYTES = 512 << 20         # bytes one rotation of step inputs must exceed (
 GRAPH_MIN_STEPS = 64           # steps per captured graph, at least
 CAL_BYTES = 256 << 20          # calibration copy size (each way) for the HBM traffic counters
 TRAFFIC_FILES = {3: ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",      # per decode config
-                 4: ROOT / "profiles" / "kqkv_decode_long_cfg4_traffic.json"}
+                 4: ROOT / "profiles" / "kqkv_decode_f16_cfg4_traffic.json"}
 
 
 def partial_kernel_name(kc_f16: bool, n_kv: int, n_split: int, q8: bool = False) -> str:
-    """The kernel the library launches for the split-K partial: an f16 cache takes the
-    barrier-per-tile kernel for splits of at most 6 64-key tiles and the independent-wave kernel
-    for longer ones (launch_kqkv_decode_f16); an f32 cache takes the VALU kernel; a Q8_0 cache its
-    own kernel (launch_kqkv_decode_q8)."""
+    """The kernel the library launches for the split-K partial of one decode row: an f16 cache
+    takes the barrier-per-tile MFMA kernel at every split length (launch_kqkv_decode_f16); an f32
+    cache the VALU kernel; a Q8_0 cache its own kernel (launch_kqkv_decode_q8)."""
     if q8:
         return "kqkv_decode_q8_kernel<576,512>"
     if not kc_f16:
         return "kqkv_generic_kernel<f32 cache>"
-    tiles_per_split = -(-(-(-n_kv // 64)) // n_split)
-    return "kqkv_decode_f16_long_kernel<576,512>" if tiles_per_split > 6 else "kqkv_decode_f16_kernel<576,512>"
+    return "kqkv_decode_f16_kernel<576,512>"
 
 
 def cpu_threads() -> dict:

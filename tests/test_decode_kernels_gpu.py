@@ -1,9 +1,8 @@
-"""GPU parity of the two split-K decode kernels and of the reference's own geometry.
+"""GPU parity of the split-K decode kernel at every split length and of the reference's own geometry.
 
-The library runs splits of a few 64-key tiles on the barrier-per-tile kernel and longer splits on
-the independent-wave kernel (the choice follows from n_kv and the split count).  These tests drive
-both through the C ABI at both instantiated geometries -- BASELINE's (D_k, D_v) = (576, 512) and
-the reference's (320, 256) (patches/ggml-m4/m4-kqkv.cu:24-40) -- on the same inputs, against the
+The library runs every decode split, of 1 to hundreds of 64-key tiles, on one barrier-per-tile
+kernel.  These tests drive it through the C ABI at both instantiated geometries -- BASELINE's
+(D_k, D_v) = (576, 512) and the reference's (320, 256) (patches/ggml-m4/m4-kqkv.cu:24-40) -- on the same inputs, against the
 CPU oracle (the unfused ggml graph) and a float64 brute force, with the tolerances of
 test_kqkv_gpu.py.  The known-answer pattern of the reference's KQKV bench
 (engine/m1_kqkv_bench.hip:148-165, tests/golden/kqkv_bench_pattern.npz, expected outputs computed
@@ -24,7 +23,6 @@ from conftest import errs, say
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "kqkv_bench_pattern.npz"
-TILES_SHORT_MAX = 6   # splits of more tiles take the independent-wave kernel
 LAZY_LOG2 = 15.0      # the kernels move a head's reference max when a tile or slice beats it by more
 
 
@@ -104,8 +102,8 @@ def make_inputs(dev, dk, n_kv, H=32, seed=7100, q_scale=0.05, holes=False):
     (320, 256, 3000, (1, 2, 16)),            # 47, 24, 3 tiles per split
 ])
 @pytest.mark.parametrize("sharp", [False, True])
-def test_short_and_long_kernels_agree_with_oracle(dev, dk, dv, n_kv, splits, sharp):
-    """sharp: q drawn with scale 300 (scores with a standard deviation of ~37 log2 units), so the
+def test_split_lengths_agree_with_oracle(dev, dk, dv, n_kv, splits, sharp):
+    """Splits of 2 to 157 tiles.  sharp: q drawn with scale 300 (scores with a standard deviation of ~37 log2 units), so the
     lazy reference maxima move and the accumulators are rescaled mid-split (counted below); with
     masked holes and a masked tail."""
     kc, q, mask, kc_d, q_d, m_d = make_inputs(dev, dk, n_kv, q_scale=300.0 if sharp else 0.05, holes=sharp)
@@ -116,7 +114,6 @@ def test_short_and_long_kernels_agree_with_oracle(dev, dk, dv, n_kv, splits, sha
     outs = {}
     for S in splits:
         tps = (n_tiles + S - 1) // S
-        kind = "long" if tps > TILES_SHORT_MAX else "short"
         if sharp:
             mv = reference_moves(kc, q, mask, scale, S)
             say(f"S={S}: {mv} reference moves after a split's first live tile")
@@ -124,9 +121,9 @@ def test_short_and_long_kernels_agree_with_oracle(dev, dk, dv, n_kv, splits, sha
         out = run_split(kc_d, q_d, m_d, scale, S, dv)
         outs[S] = out
         rel = 2e-2 if sharp else 3e-3
-        check(f"{dk}/{dv} n_kv={n_kv} S={S} ({tps} tiles/split, {kind}) sharp={sharp} vs oracle", out, ref, 1e-2, rel)
+        check(f"{dk}/{dv} n_kv={n_kv} S={S} ({tps} tiles/split) sharp={sharp} vs oracle", out, ref, 1e-2, rel)
         check(f"{dk}/{dv} S={S} sharp={sharp} vs f64 (heads 0-3)", out[:4], ref64, 1e-2, 1e-2 if sharp else 1e-3)
-    # the two kernels against each other on the same inputs
+    # the split counts against each other on the same inputs
     ss = sorted(outs)
     for a_, b_ in zip(ss, ss[1:]):
         ea, er, _ = errs(outs[a_], outs[b_])

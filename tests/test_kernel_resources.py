@@ -21,7 +21,7 @@ LDS_MAX = 160 * 1024
 # kernel name fragment -> (max VGPR spills, max scratch bytes per lane)
 BUDGET = {
     "kqkv_decode_f16_kernel": (0, 0),
-    "kqkv_decode_f16_long_kernel": (0, 0),
+    "kqkv_decode_q8_kernel": (0, 0),
     "kqkv_prefill_f16_kernel": (24, 128),
     "kqkv_generic_kernel": (0, 0),
     "merge_kernel": (0, 0),

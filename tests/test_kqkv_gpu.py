@@ -62,7 +62,7 @@ def test_split_count_invariance(dev, n_split):
 
 
 def test_cfg4_max_context(dev):
-    """262,144 keys (the long-split kernel).  All 32 heads (both 16-head halves of every
+    """262,144 keys (16 tiles per split).  All 32 heads (both 16-head halves of every
     accumulator set) against the f64 brute force at the f16-cache relative bar, and the measured
     distance to the oracle printed and bounded: the oracle rounds the normalised probabilities
     (~1/L) to f16, where they are subnormal, which puts it ~7% (relative to max) from f64 at this

@@ -37,7 +37,5 @@ def test_traffic_file_matches_its_config(config):
 
 def test_partial_kernel_name():
     assert bench.partial_kernel_name(True, 32768, 256) == "kqkv_decode_f16_kernel<576,512>"       # 2 tiles
-    assert bench.partial_kernel_name(True, 6 * 64 * 256, 256) == "kqkv_decode_f16_kernel<576,512>"  # 6 tiles
-    assert bench.partial_kernel_name(True, 6 * 64 * 256 + 1, 256) == "kqkv_decode_f16_long_kernel<576,512>"
-    assert bench.partial_kernel_name(True, 262144, 256) == "kqkv_decode_f16_long_kernel<576,512>"
+    assert bench.partial_kernel_name(True, 262144, 256) == "kqkv_decode_f16_kernel<576,512>"       # 16 tiles
     assert bench.partial_kernel_name(False, 4096, 16).startswith("kqkv_generic_kernel")
