@@ -193,7 +193,7 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) 
 }  // namespace
 
 template <int DK, int DV>
-static hipError_t launch_short(const DecodeArgs & a, int n_hgroups, hipStream_t stream) {
+static hipError_t launch_decode(const DecodeArgs & a, int n_hgroups, hipStream_t stream) {
     if (a.nt == 1)
         hipLaunchKernelGGL((kqkv_decode_f16_kernel<DK, DV, false>), dim3(a.n_split, n_hgroups, 1), dim3(NTHR), 0, stream, a);
     else
@@ -204,8 +204,8 @@ static hipError_t launch_short(const DecodeArgs & a, int n_hgroups, hipStream_t 
 
 hipError_t launch_kqkv_decode_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream) {
     const int n_hgroups = (a.n_head + decode::HG - 1) / decode::HG;
-    if (dk == 576 && dv == 512) return launch_short<576, 512>(a, n_hgroups, stream);
-    if (dk == 320 && dv == 256) return launch_short<320, 256>(a, n_hgroups, stream);
+    if (dk == 576 && dv == 512) return launch_decode<576, 512>(a, n_hgroups, stream);
+    if (dk == 320 && dv == 256) return launch_decode<320, 256>(a, n_hgroups, stream);
     return hipErrorInvalidValue;
 }
 
