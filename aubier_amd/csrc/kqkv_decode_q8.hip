@@ -251,6 +251,40 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_q8_kernel(DecodeArgs a) {
     decode_epilogue<DK, DV>(a, sh.ring8 + w * G8::SLOT, w, tid, t, hg0, sp, o, l_acc, m_ref);
 }
 
+// Q8_0 rows -> f16 rows holding the values the kernel above computes with, f16(q * d) by the same
+// instructions, for the chunked-prefill path (the f16 prefill kernel then runs on the copy).  One
+// thread per 16-value half-block: its 2-byte-aligned run read as dwords and realigned (the fifth
+// dword only when the run is misaligned, where it lies inside the row's next block), two 16-byte
+// stores.
+template <int DK>
+__global__ __launch_bounds__(256) void q8_rows_to_f16_kernel(const char * __restrict__ src, half_t * __restrict__ dst, int n_kv) {
+    using G8 = Q8Geom<DK>;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;      // half-block
+    if (i >= (int64_t)n_kv * G8::HB) return;
+    const int64_t row = i / G8::HB;
+    const int hb = (int)(i - row * G8::HB);
+    const char * r = src + row * G8::ROWB;
+    const int o = 34 * (hb >> 1) + 2 + 16 * (hb & 1);
+    const uint32_t sh = (hb & 2) ? 0u : 2u;                          // 34 b + 2 + 16 h = 2 (b + 1) mod 4
+    const uint32_t * p = reinterpret_cast<const uint32_t *>(r + (o & ~3));
+    const uint32_t wd[5] = {p[0], p[1], p[2], p[3], sh ? p[4] : 0u};
+    const half_t d = *reinterpret_cast<const half_t *>(r + 34 * (hb >> 1));
+    const half2 bias = {1152.0f16, 1152.0f16};
+    const half2 dd = {d, d};
+    uint32_t ow[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t x = __builtin_amdgcn_alignbyte(wd[k + 1], wd[k], sh) ^ 0x80808080u;
+        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
+        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+        ow[2 * k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2, lo) - bias) * dd);
+        ow[2 * k + 1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2, hi) - bias) * dd);
+    }
+    u32x4 * out = reinterpret_cast<u32x4 *>(dst + row * DK + 16 * hb);
+    out[0] = u32x4{ow[0], ow[1], ow[2], ow[3]};
+    out[1] = u32x4{ow[4], ow[5], ow[6], ow[7]};
+}
+
 template <int DK, int DV>
 hipError_t launch_q8(const DecodeArgs & a, int n_hgroups, hipStream_t stream) {
     hipLaunchKernelGGL((kqkv_decode_q8_kernel<DK, DV>), dim3(a.n_split, n_hgroups, a.nt), dim3(NTHR), 0, stream, a);
@@ -264,6 +298,15 @@ hipError_t launch_kqkv_decode_q8(int dk, int dv, const DecodeArgs & a, hipStream
     if (dk == 576 && dv == 512) return launch_q8<576, 512>(a, n_hgroups, stream);
     if (dk == 320 && dv == 256) return launch_q8<320, 256>(a, n_hgroups, stream);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_q8_rows_to_f16(int dk, const char * src, int n_kv, void * dst, hipStream_t stream) {
+    const int64_t n = (int64_t)n_kv * (dk / 16);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (dk == 576) hipLaunchKernelGGL(q8_rows_to_f16_kernel<576>, grid, dim3(256), 0, stream, src, static_cast<half_t *>(dst), n_kv);
+    else if (dk == 320) hipLaunchKernelGGL(q8_rows_to_f16_kernel<320>, grid, dim3(256), 0, stream, src, static_cast<half_t *>(dst), n_kv);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
 }
 
 }  // namespace mla

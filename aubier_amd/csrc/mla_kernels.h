@@ -67,6 +67,9 @@ bool decode_f16_supported(int dk, int dv);
 // (n_split, ceil(H/32), nt), the f16 path's partial records (f16 o) and direct output.
 hipError_t launch_kqkv_decode_q8(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
 inline bool decode_q8_supported(int dk, int dv) { return (dk == 576 && dv == 512) || (dk == 320 && dv == 256); }
+// The cache's values as f16 rows (f16(q d), the 8-bit kernel's own), dst [n_kv][dk] contiguous:
+// the chunked-prefill path over an 8-bit cache runs the f16 prefill kernel on that copy.
+hipError_t launch_q8_rows_to_f16(int dk, const char * src, int n_kv, void * dst, hipStream_t stream);
 
 // Generic VALU path (f32 or f16 cache, any D_k <= 1024, D_v <= D_k): one workgroup per
 // (split, head, token).  round16 applies the f16 rounding of q and P (F16 cache semantics).

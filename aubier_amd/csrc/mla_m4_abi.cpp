@@ -130,6 +130,18 @@ bool use_prefill(const KqkvShape & s) { return use_mfma(s) && s.nt >= mla::PREFI
 // an 8-bit (Q8_0) cache: its own MFMA kernel, one workgroup per (split, head group, token)
 bool use_q8(const KqkvShape & s) { return s.kc_type == MLA_M4_TYPE_Q8_0; }
 
+// Chunked prefill over an 8-bit cache: a pre-pass writes the cache's f16 values (f16(q d), the
+// 8-bit kernel's own) into the workspace and the f16 prefill kernel runs on that copy, 4 tokens
+// sharing every K / V tile, instead of one 8-bit decode pass over the whole window per token.
+bool use_q8_prefill(const KqkvShape & s) {
+    return use_q8(s) && s.nt >= mla::PREFILL_MIN_TOKENS && mla::decode_f16_supported((int)s.dk, (int)s.dv) &&
+           (uint64_t)s.n_kv * (uint64_t)s.dk * 2u <= 0xFFFFFFFFull;
+}
+// bytes of that copy at the head of the workspace (the partials follow it)
+size_t q8_copy_bytes(const KqkvShape & s) {
+    return use_q8_prefill(s) ? (((size_t)s.n_kv * (size_t)s.dk * 2u + 255u) & ~(size_t)255u) : 0;
+}
+
 int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
 
 // Single-token decode over an f16 cache (one 32-head group): the step is the partial and then the
@@ -149,7 +161,7 @@ int default_splits(const KqkvShape & s) {
     // the unit a split is made of: 64-key tiles (MFMA kernels), 16-key granules (VALU kernel)
     const int64_t tiles = (use_mfma(s) || use_q8(s)) ? n_tiles_of(s.n_kv) : (s.n_kv + mla::GRAN_KEYS - 1) / mla::GRAN_KEYS;
     int64_t groups;   // workgroups per split
-    if (use_prefill(s))
+    if (use_prefill(s) || use_q8_prefill(s))
         groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) *
                  ((s.nt + mla::PREFILL_TOKENS_PER_WG - 1) / mla::PREFILL_TOKENS_PER_WG);
     // decode kernels: the rows of a split share its workgroup (the launch adds row groups only
@@ -196,10 +208,11 @@ mla::DecodeArgs make_args(const mla_m4_tensor * kc, const mla_m4_tensor * q, con
     return a;
 }
 
-int launch_attn(const KqkvShape & s, const mla::DecodeArgs & a, hipStream_t stream) {
+// f16_copy: a's cache is the f16 copy of an 8-bit cache (use_q8_prefill)
+int launch_attn(const KqkvShape & s, const mla::DecodeArgs & a, hipStream_t stream, bool f16_copy = false) {
     hipError_t e;
-    if (use_q8(s)) e = mla::launch_kqkv_decode_q8((int)s.dk, (int)s.dv, a, stream);
-    else if (use_prefill(s)) e = mla::launch_kqkv_prefill_f16((int)s.dk, (int)s.dv, a, stream);
+    if (f16_copy || use_prefill(s)) e = mla::launch_kqkv_prefill_f16((int)s.dk, (int)s.dv, a, stream);
+    else if (use_q8(s)) e = mla::launch_kqkv_decode_q8((int)s.dk, (int)s.dv, a, stream);
     else if (use_mfma(s)) e = mla::launch_kqkv_decode_f16((int)s.dk, (int)s.dv, a, stream);
     else e = mla::launch_kqkv_generic((int)s.dk, (int)s.dv, s.kc_type == MLA_M4_TYPE_F16, a, stream);
     return e == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
@@ -343,17 +356,29 @@ void * scratch_ptr() {
     return g_scratch_ptr[dev];
 }
 
-// The KQKV launch sequence shared by mla_m4_kqkv and mla_m4_kqkv_noalloc: with one split the
-// attention kernel writes dst; otherwise partials into `part` (>= part_bytes(s, sp)) and the merge.
+// Workspace bytes of mla_m4_kqkv at split count sp: the f16 copy of an 8-bit cache for chunked
+// prefill, then the split-K partials.
+size_t kqkv_work_bytes(const KqkvShape & s, int sp) { return q8_copy_bytes(s) + (sp > 1 ? part_bytes(s, sp) : 0); }
+
+// The KQKV launch sequence shared by mla_m4_kqkv and mla_m4_kqkv_noalloc, over `work` (>=
+// kqkv_work_bytes(s, sp)): for chunked prefill over an 8-bit cache, its f16 copy first; then with
+// one split the attention kernel writes dst, otherwise partials and the merge.
 int kqkv_launch(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask, float kq_scale,
-                const mla_m4_tensor * dst, const KqkvShape & s, int sp, char * part, hipStream_t st) {
+                const mla_m4_tensor * dst, const KqkvShape & s, int sp, char * work, hipStream_t st) {
     mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, sp);
+    const bool f16_copy = use_q8_prefill(s);
+    if (f16_copy) {
+        if (mla::launch_q8_rows_to_f16((int)s.dk, a.kc, (int)s.n_kv, work, st) != hipSuccess) return MLA_M4_ERR_LAUNCH;
+        a.kc = work;
+        a.kc_nb1 = s.dk * 2;
+    }
+    char * part = work + q8_copy_bytes(s);
     if (sp == 1) {
         a.dst = static_cast<float *>(dst->data);
-        return launch_attn(s, a, st);
+        return launch_attn(s, a, st, f16_copy);
     }
     a.part = part;
-    const int rc = launch_attn(s, a, st);
+    const int rc = launch_attn(s, a, st, f16_copy);
     if (rc != MLA_M4_OK) return rc;
     return mla::launch_merge(a.part, (int)s.dv, part_o_bytes(s), sp, (int)s.nt, (int)s.n_head, static_cast<float *>(dst->data), st) == hipSuccess
                ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
@@ -407,7 +432,7 @@ size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_te
     KqkvShape s{};
     if (check_kqkv(kcache, q, nullptr, dst, &s) != MLA_M4_OK) return 0;
     const int sp = (s.dv & 7) ? 1 : default_splits(s);
-    return sp > 1 ? part_bytes(s, sp) : 0;
+    return kqkv_work_bytes(s, sp);
 }
 
 int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type) {
@@ -424,7 +449,8 @@ int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla
     if (rc != MLA_M4_OK) return rc;
     if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
     const int sp = (s.dv & 7) ? 1 : default_splits(s);     // the merge reads 8 columns at a time
-    if (sp > 1 && (!workspace || !aligned16(workspace) || workspace_bytes < part_bytes(s, sp))) return MLA_M4_ERR_WORKSPACE;
+    const size_t need = kqkv_work_bytes(s, sp);
+    if (need > 0 && (!workspace || !aligned16(workspace) || workspace_bytes < need)) return MLA_M4_ERR_WORKSPACE;
     return kqkv_launch(kcache, q, mask, kq_scale, dst, s, sp, static_cast<char *>(workspace), static_cast<hipStream_t>(stream));
 }
 
@@ -435,13 +461,14 @@ int mla_m4_kqkv_noalloc(const mla_m4_tensor * kcache, const mla_m4_tensor * q, c
     if (rc != MLA_M4_OK) return rc;
     if (!std::isfinite(kq_scale)) return MLA_M4_ERR_ARG;
     const int sp = (s.dv & 7) ? 1 : default_splits(s);
-    char * part = nullptr;
-    if (sp > 1) {
-        if (part_bytes(s, sp) > MLA_M4_NOALLOC_SCRATCH_BYTES) return MLA_M4_ERR_SCRATCH;
-        part = static_cast<char *>(scratch_ptr());
-        if (part == nullptr) return MLA_M4_ERR_SCRATCH;
+    const size_t need = kqkv_work_bytes(s, sp);
+    char * work = nullptr;
+    if (need > 0) {
+        if (need > MLA_M4_NOALLOC_SCRATCH_BYTES) return MLA_M4_ERR_SCRATCH;
+        work = static_cast<char *>(scratch_ptr());
+        if (work == nullptr) return MLA_M4_ERR_SCRATCH;
     }
-    return kqkv_launch(kcache, q, mask, kq_scale, dst, s, sp, part, static_cast<hipStream_t>(stream));
+    return kqkv_launch(kcache, q, mask, kq_scale, dst, s, sp, work, static_cast<hipStream_t>(stream));
 }
 
 int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask,

@@ -358,7 +358,7 @@ def main() -> int:
         inp = I.make_batch(args.batch, region, lens=[region] * args.batch)
     else:
         inp = I.make_config(args.config)
-        if args.cache == "q8" and inp.nt == 1:
+        if args.cache == "q8":
             inp = I.with_q8_cache(inp)
         if inp.nt > 1:
             rec = prefill_record(inp, args.steps, args.warmup, cpu=not args.no_cpu, cpu_thr=cpu_threads()["threads"])
@@ -458,13 +458,19 @@ def pmc_pass(inp, args) -> int:
 
 def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = False) -> dict:
     """Config 5 (chunked prefill, nt > 1): WKB -> KQKV through ggml_m4_kqkv, MFMA-bound, reported
-    in TFLOP/s of exact causal work against the f16 dense MFMA peak.  Not the headline metric."""
+    in TFLOP/s of exact causal work against the f16 dense MFMA peak.  Not the headline metric.
+    Over an 8-bit cache (--cache q8) the op first writes the cache's f16 values into its workspace;
+    its attention figure is then the whole op (copy + attention + merge)."""
     import torch
     import aubier_amd as A
     from aubier_amd import inputs as I
     dev = torch.device("cuda:0")
     H, DV, DK, T = I.N_HEAD, I.D_V, I.D_K, inp.nt
-    kc = torch.from_numpy(np.ascontiguousarray(inp.kcache)).to(dev)
+    q8 = inp.kcache_q8 is not None
+    if q8:
+        kc = A.Q8_0(torch.from_numpy(np.ascontiguousarray(inp.kcache_q8)).to(dev), DK)
+    else:
+        kc = torch.from_numpy(np.ascontiguousarray(inp.kcache)).to(dev)
     wkb_w = torch.from_numpy(inp.w_kb).to(dev)
     q = np.concatenate([inp.q_nope, inp.q_pe], axis=2).astype(np.float32)
     qd = torch.from_numpy(q).to(dev)
@@ -507,7 +513,9 @@ def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = F
 
     part = None
     n_split = max(1, need // (((H + 31) // 32) * T * A.ops.part_floats(DV, inp.kc_f16) * 4)) if need else 1
-    if n_split > 1:
+    if q8:
+        n_split = None                       # the op's own split count, behind its f16 copy
+    elif n_split > 1:
         part = torch.empty(((H + 31) // 32, T, n_split, A.ops.part_floats(DV, inp.kc_f16)), dtype=torch.float32, device=dev)
     # per kernel: 12 replays of a 4-launch graph (fewer read low right after another config's run)
     KR = 12
@@ -517,7 +525,7 @@ def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = F
         us_merge = time_fn(lambda: A.ggml_m4_phase_merge(part, out=out), KR)
     else:
         us_attn = time_fn(lambda: A.ggml_m4_kqkv(kc, qcur, mask, inp.kq_scale, out=out, workspace=ws), KR)
-        us_merge = 0.0
+        us_merge = None if q8 else 0.0
     step()
     torch.cuda.synchronize()
     got = out.cpu().numpy()
@@ -533,24 +541,26 @@ def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = F
                    "sample": "config 5 full step (WKB + unfused kq/softmax/kqv), one run"}
         err = errors(got, ref)
     if nested:
-        return {"n_kv": inp.n_kv, "nt": T, "splits": n_split, "cache": "f16", "steps": reps * NG, "warmup": warmup,
+        return {"n_kv": inp.n_kv, "nt": T, "splits": n_split, "cache": "q8_0" if q8 else "f16", "steps": reps * NG, "warmup": warmup,
                 "us_step": round(us, 2), "tflops_step": round(tf, 1), "frac_of_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                "us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2), "us_phase_merge": round(us_merge, 2),
-                "attention_tflops": round(tf_attn, 1), "attention_frac_of_mfma_peak": round(tf_attn / MFMA_F16_PEAK_TFLOPS, 4),
+                "us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2),
+                "us_phase_merge": None if us_merge is None else round(us_merge, 2), "attention_tflops": round(tf_attn, 1), "attention_frac_of_mfma_peak": round(tf_attn / MFMA_F16_PEAK_TFLOPS, 4),
                 "gflop_per_step": round(flop / 1e9, 2),
                 "cpu_ms": round(cpu_rec["value"] / 1e3, 3) if cpu_rec else None, "cpu_threads": cpu_thr if cpu_rec else None,
                 "err_vs_oracle": err}
     return {"metric": "MLA chunked prefill (config 5): us/step and TFLOP/s of exact causal work", "value": round(us, 2),
             "unit": "us/step", "n_gpus": 1, "steps": reps * NG, "warmup": warmup, "ms_per_step": round(us / 1000.0, 4),
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-            "config": {"workload": f"config 5: {T} tokens x {inp.n_kv} keys causal, 32 heads, f16 cache", "nt": T,
+            "config": {"workload": f"config 5: {T} tokens x {inp.n_kv} keys causal, 32 heads, "
+                                   + ("Q8_0 cache (f16 copy in the workspace)" if q8 else "f16 cache"), "nt": T,
                        "n_kv": inp.n_kv},
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None, "gflop_per_step": round(flop / 1e9, 2),
                          "attention_kernel": {"us": round(us_attn, 2), "tflops": round(tf_attn, 1),
                                               "frac": round(tf_attn / MFMA_F16_PEAK_TFLOPS, 4), "splits": n_split}},
             "cpu_baseline": cpu_rec,
-            "extra": {"us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2), "us_phase_merge": round(us_merge, 2),
+            "extra": {"us_wkb": round(us_wkb, 2), "us_kqkv_partial": round(us_attn, 2),
+                      "us_phase_merge": None if us_merge is None else round(us_merge, 2),
                       "err_vs_oracle": err}}
 
 

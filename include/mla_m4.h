@@ -134,14 +134,18 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
  * score minus a running reference max, at most 2^15) -- ggml-cpu rounds the normalised P instead,
  * which is subnormal in f16 at long context, so results differ from the oracle by more than one
  * rounding there (and are closer to exact arithmetic); an F32 cache runs in f32.
- * nt == 1 is split-K decode (partial + merge, two launches); nt > 1 is the prefill path.
- * `workspace` (device memory, >= mla_m4_kqkv_workspace_bytes()) holds the split-K partials.
+ * Up to 15 tokens (nt) run the decode kernels, split-K (partial + merge, two launches); from 16
+ * tokens the prefill kernel (4 tokens per workgroup sharing each K/V tile).
+ * `workspace` (device memory, >= mla_m4_kqkv_workspace_bytes()) holds the split-K partials, and,
+ * for 16 or more tokens over a Q8_0 cache, first the cache's f16 values (n_kv x D_k x 2 bytes,
+ * rounded up to 256), which the f16 prefill kernel then reads (a third launch before it).
  * ------------------------------------------------------------------------------------------- */
 int mla_m4_kqkv(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
                 const mla_m4_tensor * mask, float kq_scale, const mla_m4_tensor * dst,
                 void * workspace, size_t workspace_bytes, void * stream);
 
-/* Workspace bytes mla_m4_kqkv needs for these shapes (0 when no partials are used). */
+/* Workspace bytes mla_m4_kqkv needs for these shapes: the split-K partials, plus the f16 copy of a
+ * Q8_0 cache for 16 or more tokens (0 when neither is used). */
 size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
                                    const mla_m4_tensor * dst);
 
@@ -152,11 +156,12 @@ size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_te
  * split-K partials live in a static device array of MLA_M4_NOALLOC_SCRATCH_BYTES (32 MiB) that
  * each GPU the library runs on holds until the process ends.  With an f16 cache a 32-head group
  * at 256 splits (>= 16K keys) needs 8.45 MB per token, so decode of up to 3 tokens at H <= 32
- * fits; the f32-cache kernel uses ~256 / (H nt) splits (0.53 MB at H = 32, one token).  Shapes
- * that need more (prefill, more heads) return MLA_M4_ERR_SCRATCH.  Allocates nothing and calls
- * no allocating routine; the first call on each device resolves the array's address
- * (hipGetSymbolAddress), so make that first call outside graph capture.  Every call on a GPU uses that GPU's one array: calls that overlap on one GPU
- * (concurrent streams) race.
+ * fits; the f32-cache kernel uses ~256 / (H nt) splits (0.53 MB at H = 32, one token).  The
+ * workspace a shape needs (mla_m4_kqkv_workspace_bytes, including a Q8_0 cache's f16 copy for
+ * prefill) must fit the array; larger shapes (long prefill, more heads) return MLA_M4_ERR_SCRATCH.
+ * Allocates nothing and calls no allocating routine; the first call on each device resolves the
+ * array's address (hipGetSymbolAddress), so make that first call outside graph capture.  Every
+ * call on a GPU uses that GPU's one array: calls that overlap on one GPU (concurrent streams) race.
  * ------------------------------------------------------------------------------------------- */
 #define MLA_M4_NOALLOC_SCRATCH_BYTES (32u << 20)
 int mla_m4_kqkv_noalloc(const mla_m4_tensor * kcache, const mla_m4_tensor * q,

@@ -272,3 +272,17 @@ def test_supports_kqkv_q8_cache():
     assert S == 256
     _, q, _, out = decode_tensors(n_kv=32768)
     assert A.kqkv_workspace_bytes(q8((32768,), 576), q, out) == S * ops.part_floats(512, True) * 4
+
+
+@pytest.mark.parametrize("dk,dv", [(576, 512), (320, 256)])
+def test_q8_prefill_workspace_holds_the_f16_copy(dk, dv):
+    """From 16 tokens KQKV over an 8-bit cache runs the f16 prefill kernel on an f16 copy of the
+    cache at the head of its workspace (256-byte rounded), the partials after it, at the f16
+    prefill's own split count; below 16 tokens (the 8-bit decode kernel) there is no copy."""
+    for n_kv in (1500, 8192):
+        kc16, q, _, out = decode_tensors(n_kv=n_kv, nt=20, dk=dk, dv=dv)
+        copy = (n_kv * dk * 2 + 255) // 256 * 256
+        assert A.kqkv_workspace_bytes(q8((n_kv,), dk), q, out) == copy + A.kqkv_workspace_bytes(kc16, q, out)
+    kc16, q, _, out = decode_tensors(n_kv=1500, nt=15, dk=dk, dv=dv)
+    S = -(-256 // 15)                       # the 8-bit decode kernel: ~256 workgroups over 15 rows
+    assert A.kqkv_workspace_bytes(q8((1500,), dk), q, out) == 15 * S * ops.part_floats(dv, True) * 4

@@ -13,6 +13,9 @@ The cache is quantised by ggml's quantize_row_q8_0_ref (oracle.q8_0_quantize, pi
 test_oracle_q8.py).  Cases: config 3's 32K-key step, the single-split direct path, ragged windows
 with masked holes and a masked tail, long splits (the int8 ring cycling over many tiles), the
 reference's (320, 256) geometry, several rows, and sharp scores that move the lazy reference max.
+From 16 tokens (chunked prefill) the op runs the f16 prefill kernel on an f16 copy of the cache
+that it writes into its workspace: those results must equal the op over an F16 cache holding the
+same values bit for bit.
 """
 import numpy as np
 import pytest
@@ -118,20 +121,62 @@ def test_q8_cache_cases(dev, dk, dv, n_kv, nt, splits, holes, q_scale):
         assert eq <= bound
 
 
-def test_q8_cache_chunked_prefill(dev):
-    """A chunk of 20 tokens over a Q8_0 cache with a causal mask (token i sees the cached keys and
-    new keys up to its own): the 8-bit kernel runs one workgroup per token (no token batching, so
-    prefill over an 8-bit cache is correct but not the MFMA prefill kernel's speed)."""
-    n_kv, nt, dk, dv, H = 1500, 20, 576, 512, 32
-    kc = I.randn(7400, n_kv * dk).astype(np.float16).reshape(n_kv, dk)
-    q = I.randn(7401, nt * H * dk, 0.05).reshape(nt, H, dk)
+def causal_chunk(n_kv, nt, dk, H, seed):
+    kc = I.randn(seed, n_kv * dk).astype(np.float16).reshape(n_kv, dk)
+    q = I.randn(seed + 1, nt * H * dk, 0.05).reshape(nt, H, dk)
     mask = np.zeros((nt, n_kv), dtype=np.float32)
     for t in range(nt):
         mask[t, n_kv - nt + t + 1:] = -np.inf
+    return kc, q, mask
+
+
+@pytest.mark.parametrize("dk,dv", [(576, 512), (320, 256)])
+def test_q8_cache_chunked_prefill(dev, dk, dv):
+    """A chunk of 20 tokens over a Q8_0 cache with a causal mask (token i sees the cached keys and
+    new keys up to its own).  From 16 tokens the op writes the cache's f16 values into its
+    workspace and runs the f16 prefill kernel on them: the result is bit-identical to the op over
+    an F16 cache holding those values, and within the f16 bars of the oracle."""
+    n_kv, nt, H = 1500, 20, 32
+    kc, q, mask = causal_chunk(n_kv, nt, dk, H, 7400)
     _, deq, kq = q8_cache(kc, dev)
+    q_d, m_d = torch.from_numpy(q).to(dev), torch.from_numpy(mask).to(dev)
     ref = orc.kqkv(deq, q, mask, SCALE, d_v=dv)
-    out = run(kq, torch.from_numpy(q).to(dev), torch.from_numpy(mask).to(dev), None, dv)
-    check("q8 chunked prefill nt=20 vs oracle(dequantised)", out, ref, 1e-2, 3e-3)
+    out = run(kq, q_d, m_d, None, dv)
+    check(f"q8 chunked prefill {dk}/{dv} nt=20 vs oracle(dequantised)", out, ref, 1e-2, 3e-3)
+    via_f16 = run(torch.from_numpy(deq).to(dev), q_d, m_d, None, dv)
+    assert np.array_equal(out, via_f16)
+    # the explicit-split entry point keeps the per-token 8-bit kernel: same bars
+    out_p = run(kq, q_d, m_d, 7, dv)
+    check(f"q8 chunked prefill {dk}/{dv} nt=20 S=7 (8-bit kernel) vs oracle(dequantised)", out_p, ref, 1e-2, 3e-3)
+
+
+def test_q8_cache_prefill_config5_shape(dev):
+    """Config 5's shape (512 tokens x 8,192 keys, causal) over a Q8_0 cache: bit-identical to the
+    op over the dequantised F16 cache, and the first and last 8 tokens against the oracle."""
+    n_kv, nt, dk, dv, H = 8192, 512, 576, 512, 32
+    kc, q, mask = causal_chunk(n_kv, nt, dk, H, 7500)
+    _, deq, kq = q8_cache(kc, dev)
+    q_d, m_d = torch.from_numpy(q).to(dev), torch.from_numpy(mask).to(dev)
+    out = run(kq, q_d, m_d, None, dv)
+    via_f16 = run(torch.from_numpy(deq).to(dev), q_d, m_d, None, dv)
+    assert np.array_equal(out, via_f16)
+    for sl in (slice(0, 8), slice(nt - 8, nt)):
+        ref = orc.kqkv(deq, np.ascontiguousarray(q[sl]), np.ascontiguousarray(mask[sl]), SCALE, d_v=dv)
+        check(f"q8 prefill 512 x 8192, tokens {sl.start}..{sl.stop - 1} vs oracle(dequantised)", out[:, sl], ref, 1e-2, 3e-3)
+
+
+def test_q8_cache_prefill_noalloc_matches(dev):
+    """The no-allocation entry point over a Q8_0 prefill chunk whose f16 copy and partials fit
+    its scratch (1.2 MB of copy, 16 splits x 16 tokens of partials): bit-identical with
+    ggml_m4_kqkv."""
+    n_kv, nt, dk, H = 1024, 16, 576, 32
+    kc, q, mask = causal_chunk(n_kv, nt, dk, H, 7600)
+    _, _, kq = q8_cache(kc, dev)
+    q_d, m_d = torch.from_numpy(q).to(dev), torch.from_numpy(mask).to(dev)
+    a = A.ggml_m4_kqkv(kq, q_d, m_d, SCALE)
+    b = A.ggml_m4_kqkv_noalloc(kq, q_d, m_d, SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
 
 
 def test_q8_cache_noalloc_matches(dev):
