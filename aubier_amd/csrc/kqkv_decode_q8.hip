@@ -23,8 +23,10 @@
 // LDS at D_k = 576: int8 ring 2 x 4 x (9,792 + 256) + f16 tile 4 x 18,688 + P exchange 4,608 +
 // slice maxima 1,024 = 160,768 bytes.
 //
-// Grid = (n_split, ceil(H/32), nt), 256 threads; the output is the f16 path's: partial blocks
-// [group][token][split] with f16 o, or o/l in f32 to dst with one split.
+// Grid = (n_split, ceil(H/32), row groups), 256 threads; the rows of a split share its workgroup as
+// in kqkv_decode.hip (decode_row_groups), and a row with no live key in the split records an empty
+// split.  The output is the f16 path's: partial blocks [group][token][split] with f16 o, or o/l in
+// f32 to dst with one split.
 #include "decode_common.h"
 
 namespace mla {
@@ -125,19 +127,18 @@ __device__ __forceinline__ void dequant_slice(const char * src, char * dst, int 
     }
 }
 
+// One row (token) t of the split: the whole pass, from the q staging to the partial record.
 template <int DK, int DV>
-__global__ __launch_bounds__(NTHR, 1) void kqkv_decode_q8_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_row_q8(const DecodeArgs & a, int t, Q8Lds<DK, DV> & sh) {
     using G = SliceGeom<DK>;
     using G8 = Q8Geom<DK>;
     using C = ShortCfg<DK, DV>;
-    __shared__ Q8Lds<DK, DV> sh;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sp = blockIdx.x;
     const int hg0 = blockIdx.y * HG;
-    const int t = blockIdx.z;
     const int g = lane >> 4;
     const int j16 = lane & 15;
 
@@ -251,6 +252,39 @@ __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_q8_kernel(DecodeArgs a) {
     decode_epilogue<DK, DV>(a, sh.ring8 + w * G8::SLOT, w, tid, t, hg0, sp, o, l_acc, m_ref);
 }
 
+// ROWS = false: one row per workgroup (blockIdx.z).  ROWS = true: rows blockIdx.z, blockIdx.z +
+// gridDim.z, ... of split blockIdx.x share the workgroup (batch-of-N decode puts every row of a
+// split in one); with a mask, the rows that hold no live key of the split are found first, in
+// rounds of a few tiles of mask reads, and only record an empty split, the others run the whole
+// pass in turn.  As kqkv_decode_f16_kernel.
+template <int DK, int DV, bool ROWS>
+__global__ __launch_bounds__(NTHR, 1) void kqkv_decode_q8_kernel(DecodeArgs a) {
+    __shared__ Q8Lds<DK, DV> sh;
+    if constexpr (!ROWS) {
+        decode_row_q8<DK, DV>(a, blockIdx.z, sh);
+        return;
+    }
+    __shared__ uint32_t live_w[NWAVE];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint32_t live = ~0u;
+    if (a.nt > 1 && a.dst == nullptr && a.mask != nullptr) {
+        const uint32_t bits = live_rows_of_wave<LIVE_ROUND_TILES>(a, blockIdx.x, w, lane);
+        if (lane == 0) live_w[w] = bits;
+        __syncthreads();
+        live = live_w[0] | live_w[1] | live_w[2] | live_w[3];
+    }
+    int i = 0;
+    for (int t = blockIdx.z; t < a.nt; t += gridDim.z, ++i) {
+        if (!((live >> i) & 1u)) {
+            if (w == 0) write_empty_pairs(a, blockIdx.y, t, blockIdx.x, DV, lane);
+            continue;
+        }
+        decode_row_q8<DK, DV>(a, t, sh);
+        __syncthreads();                     // the next row's staging reuses the LDS
+    }
+}
+
 // Q8_0 rows -> f16 rows holding the values the kernel above computes with, f16(q * d) by the same
 // instructions, for the chunked-prefill path (the f16 prefill kernel then runs on the copy).  One
 // thread per 16-value half-block: its 2-byte-aligned run read as dwords and realigned (the fifth
@@ -287,7 +321,11 @@ __global__ __launch_bounds__(256) void q8_rows_to_f16_kernel(const char * __rest
 
 template <int DK, int DV>
 hipError_t launch_q8(const DecodeArgs & a, int n_hgroups, hipStream_t stream) {
-    hipLaunchKernelGGL((kqkv_decode_q8_kernel<DK, DV>), dim3(a.n_split, n_hgroups, a.nt), dim3(NTHR), 0, stream, a);
+    if (a.nt == 1)
+        hipLaunchKernelGGL((kqkv_decode_q8_kernel<DK, DV, false>), dim3(a.n_split, n_hgroups, 1), dim3(NTHR), 0, stream, a);
+    else
+        hipLaunchKernelGGL((kqkv_decode_q8_kernel<DK, DV, true>), dim3(a.n_split, n_hgroups, decode_row_groups(a, n_hgroups)),
+                           dim3(NTHR), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -64,7 +64,8 @@ constexpr int PREFILL_TOKENS_PER_WG = 4;
 hipError_t launch_kqkv_prefill_f16(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
 bool decode_f16_supported(int dk, int dv);
 // An 8-bit cache (ggml block_q8_0 rows, contiguous): the decode kernel of kqkv_decode_q8.hip, grid
-// (n_split, ceil(H/32), nt), the f16 path's partial records (f16 o) and direct output.
+// (n_split, ceil(H/32), row groups) as the f16 decode kernel, the f16 path's partial records (f16 o)
+// and direct output.
 hipError_t launch_kqkv_decode_q8(int dk, int dv, const DecodeArgs & a, hipStream_t stream);
 inline bool decode_q8_supported(int dk, int dv) { return (dk == 576 && dv == 512) || (dk == 320 && dv == 256); }
 // The cache's values as f16 rows (f16(q d), the 8-bit kernel's own), dst [n_kv][dk] contiguous:

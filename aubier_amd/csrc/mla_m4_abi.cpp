@@ -127,7 +127,8 @@ bool use_mfma(const KqkvShape & s) {
 // several tokens on the MFMA path: the prefill kernel (4 tokens per workgroup share each tile)
 bool use_prefill(const KqkvShape & s) { return use_mfma(s) && s.nt >= mla::PREFILL_MIN_TOKENS; }
 
-// an 8-bit (Q8_0) cache: its own MFMA kernel, one workgroup per (split, head group, token)
+// an 8-bit (Q8_0) cache: its own MFMA kernel, one workgroup per (split, head group), shared by the
+// split's rows as in the f16 decode kernel
 bool use_q8(const KqkvShape & s) { return s.kc_type == MLA_M4_TYPE_Q8_0; }
 
 // Chunked prefill over an 8-bit cache: a pre-pass writes the cache's f16 values (f16(q d), the
@@ -166,8 +167,7 @@ int default_splits(const KqkvShape & s) {
                  ((s.nt + mla::PREFILL_TOKENS_PER_WG - 1) / mla::PREFILL_TOKENS_PER_WG);
     // decode kernels: the rows of a split share its workgroup (the launch adds row groups only
     // when there are few splits), so the split count is the single-row one
-    else if (use_mfma(s)) groups = (s.n_head + DECODE_HEADS - 1) / DECODE_HEADS;
-    else if (use_q8(s)) groups = ((s.n_head + DECODE_HEADS - 1) / DECODE_HEADS) * s.nt;
+    else if (use_mfma(s) || use_q8(s)) groups = (s.n_head + DECODE_HEADS - 1) / DECODE_HEADS;
     else groups = s.n_head * s.nt;
     int64_t sp = (TARGET_WG + groups - 1) / groups;
     if (use_mfma(s) && !use_prefill(s) && s.nt == 1 && groups == 1) sp = decode_f16_step_splits(tiles);

@@ -356,6 +356,8 @@ def main() -> int:
     if args.batch:
         region = 32768 // args.batch
         inp = I.make_batch(args.batch, region, lens=[region] * args.batch)
+        if args.cache == "q8":
+            inp = I.with_q8_cache(inp)
     else:
         inp = I.make_config(args.config)
         if args.cache == "q8":

@@ -284,5 +284,5 @@ def test_q8_prefill_workspace_holds_the_f16_copy(dk, dv):
         copy = (n_kv * dk * 2 + 255) // 256 * 256
         assert A.kqkv_workspace_bytes(q8((n_kv,), dk), q, out) == copy + A.kqkv_workspace_bytes(kc16, q, out)
     kc16, q, _, out = decode_tensors(n_kv=1500, nt=15, dk=dk, dv=dv)
-    S = -(-256 // 15)                       # the 8-bit decode kernel: ~256 workgroups over 15 rows
+    S = A.default_splits(1500, 32, ops.TYPE_Q8_0)   # the 8-bit decode kernel: the single-row count
     assert A.kqkv_workspace_bytes(q8((1500,), dk), q, out) == 15 * S * ops.part_floats(dv, True) * 4

@@ -130,6 +130,20 @@ def causal_chunk(n_kv, nt, dk, H, seed):
     return kc, q, mask
 
 
+@pytest.mark.parametrize("n_seq,region,splits", [(4, 2048, (None, 3)), (8, 1536, (None, 64))])
+def test_q8_cache_batch_decode(dev, n_seq, region, splits):
+    """Batch-of-N decode over per-sequence regions (inputs.make_batch) of a Q8_0 cache: each row's
+    splits outside its region record empty splits; against the oracle on the dequantised cache."""
+    inp = I.make_batch(n_seq, region)
+    _, deq, kq = q8_cache(inp.kcache, dev)
+    q = I.randn(7700 + n_seq, n_seq * 32 * 576, 0.05).reshape(n_seq, 32, 576)
+    q_d, m_d = torch.from_numpy(q).to(dev), torch.from_numpy(inp.mask).to(dev)
+    ref = orc.kqkv(deq, q, inp.mask, SCALE)
+    for S in splits:
+        out = run(kq, q_d, m_d, S, 512)
+        check(f"q8 batch N={n_seq} x {region} S={S} vs oracle(dequantised)", out, ref, 1e-2, 3e-3)
+
+
 @pytest.mark.parametrize("dk,dv", [(576, 512), (320, 256)])
 def test_q8_cache_chunked_prefill(dev, dk, dv):
     """A chunk of 20 tokens over a Q8_0 cache with a causal mask (token i sees the cached keys and
