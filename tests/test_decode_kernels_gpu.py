@@ -161,7 +161,7 @@ def test_prefill_kernel_causal(dev, dk, dv, n_kv, nt, splits, q_scale):
 
 @pytest.mark.parametrize("dk,dv,n_kv,nt,S", [
     (576, 512, 8192, 1, 64),      # barrier-per-tile kernel (2 tiles per split): splits 0-31 fully masked
-    (576, 512, 8192, 1, 8),       # independent-wave kernel (16 tiles per split): splits 0-3
+    (576, 512, 8192, 1, 8),       # long splits (16 tiles per split): splits 0-3
     (576, 512, 4096, 3, 16),      # batch-of-N rows on the barrier-per-tile kernel
     (576, 512, 4096, 20, 4),      # prefill kernel (nt >= 16): splits 0-1
     (320, 256, 4096, 1, 32),
