@@ -121,6 +121,23 @@ def test_q8_cache_cases(dev, dk, dv, n_kv, nt, splits, holes, q_scale):
         assert eq <= bound
 
 
+def test_q8_cache_max_context(dev):
+    """Config 4's window (262,144 keys, 16 tiles per split, its masked tail of 1000-valued rows)
+    quantised to Q8_0: all 32 heads against the float64 brute force on the dequantised values at
+    the f16-cache relative bar (1e-3), and against the F16-cache op over those same values."""
+    inp = I.make_config(4)
+    _, deq, kq = q8_cache(inp.kcache, dev)
+    q = I.randn(7800, 32 * 576, 0.05).reshape(1, 32, 576)
+    q_d, m_d = torch.from_numpy(q).to(dev), torch.from_numpy(inp.mask).to(dev)
+    out = run(kq, q_d, m_d, None, 512)
+    ref64 = orc.attn_f64(deq, q, inp.mask, SCALE)
+    ea, er, rr = errs(out, ref64)
+    say(f"q8 262,144 keys vs f64(dequantised): max_abs={ea:.3e} max_rel={er:.3e} rms_rel={rr:.3e}")
+    assert np.isfinite(out).all() and er <= 1e-3
+    via_f16 = run(torch.from_numpy(deq).to(dev), q_d, m_d, None, 512)
+    check("q8 262,144 keys vs the F16 op on the same values", out, via_f16, 1e-2, 1e-3)
+
+
 def causal_chunk(n_kv, nt, dk, H, seed):
     kc = I.randn(seed, n_kv * dk).astype(np.float16).reshape(n_kv, dk)
     q = I.randn(seed + 1, nt * H * dk, 0.05).reshape(nt, H, dk)
