@@ -455,7 +455,7 @@ template <int DK>
 __device__ __forceinline__ constexpr int stage_byte(int s, int v) { return (s * NWAVE + v) * SliceGeom<DK>::STAGE; }
 
 template <int DK, int DV>
-struct ShortCfg {
+struct DecodeCfg {
     using G = SliceGeom<DK>;
     static_assert(DV % 128 == 0 && DV <= DK, "geometry");
     static constexpr int DVQ = DV / NWAVE;              // output columns per wave
@@ -470,9 +470,9 @@ struct ShortCfg {
 
 // LDS of the kernel: the slice ring, the P exchange and the slice maxima, by tile parity
 template <int DK, int DV>
-struct ShortLds {
+struct DecodeLds {
     __attribute__((aligned(16))) char ring[SliceGeom<DK>::RING];       // [stage][wave] K rows + mask
-    __attribute__((aligned(16))) half_t px[2][HG * ShortCfg<DK, DV>::PROW];
+    __attribute__((aligned(16))) half_t px[2][HG * DecodeCfg<DK, DV>::PROW];
     __attribute__((aligned(16))) float red[2][HG][NWAVE];              // [head][wave]
 };
 
@@ -483,8 +483,8 @@ struct ShortLds {
 // keys 8 (lane >> 5) .. +7 of each slice).
 template <int DK, int DV>
 __device__ __forceinline__ void pv_tile(const char * ring, const half_t * pxv, int par, int w, int lane, const PvAddr & pv,
-                                        f32x16 (&o)[ShortCfg<DK, DV>::NTQ], float & l_acc) {
-    using C = ShortCfg<DK, DV>;
+                                        f32x16 (&o)[DecodeCfg<DK, DV>::NTQ], float & l_acc) {
+    using C = DecodeCfg<DK, DV>;
     {
         half8 pa[2], vb[2][C::NTQ];
         auto load = [&](int ks, int b) {
@@ -515,9 +515,9 @@ __device__ __forceinline__ void pv_tile(const char * ring, const half_t * pxv, i
 // No workgroup barrier: every wave holds its own heads' l.
 template <int DK, int DV>
 __device__ __forceinline__ void decode_epilogue(const DecodeArgs & a, char * stg, int w, int tid, int t, int hg0,
-                                                int sp, f32x16 (&o)[ShortCfg<DK, DV>::NTQ], float l_acc,
+                                                int sp, f32x16 (&o)[DecodeCfg<DK, DV>::NTQ], float l_acc,
                                                 const float (&m_ref)[2]) {
-    using C = ShortCfg<DK, DV>;
+    using C = DecodeCfg<DK, DV>;
     // thread indices re-derived through an opaque move, so that the epilogue's address arithmetic
     // is computed here rather than before the loop and kept alive (or spilled) across it
     int tid_e;

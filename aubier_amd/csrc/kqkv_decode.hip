@@ -41,9 +41,9 @@ using namespace decode;
 
 // One row (token) t of the split: the whole pass, from the q staging to the partial record.
 template <int DK, int DV>
-__device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds<DK, DV> & sh) {
+__device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, DecodeLds<DK, DV> & sh) {
     using G = SliceGeom<DK>;
-    using C = ShortCfg<DK, DV>;
+    using C = DecodeCfg<DK, DV>;
     char (&ring)[G::RING] = sh.ring;
     half_t (&px)[2][HG * C::PROW] = sh.px;
     float (&red)[2][HG][NWAVE] = sh.red;
@@ -164,7 +164,7 @@ __device__ __forceinline__ void decode_row(const DecodeArgs & a, int t, ShortLds
 // pass in turn.
 template <int DK, int DV, bool ROWS>
 __global__ __launch_bounds__(NTHR, 1) void kqkv_decode_f16_kernel(DecodeArgs a) {
-    __shared__ ShortLds<DK, DV> sh;
+    __shared__ DecodeLds<DK, DV> sh;
     if constexpr (!ROWS) {
         decode_row<DK, DV>(a, blockIdx.z, sh);
         return;

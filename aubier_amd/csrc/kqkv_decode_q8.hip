@@ -6,7 +6,7 @@
 // F16 (its KQKV asserts it: patches/ggml-m4/m4-kqkv.cu:345); this is the same op over the smaller
 // cache, with the partial records and the merge of the f16 path.
 //
-// Design: the f16 short decode kernel's Q.K^T / softmax / P.V (decode_common.h, kqkv_decode.hip) on
+// Design: the f16 decode kernel's Q.K^T / softmax / P.V (decode_common.h, kqkv_decode.hip) on
 // a single f16 tile that the four waves fill by dequantising their slices:
 //   * wave w streams its 16-key slice of every tile (16 rows: one contiguous, 16-byte-aligned run)
 //     with its 16 mask values into its own slot of a two-stage int8 ring by LDS DMA.  The first two
@@ -53,9 +53,9 @@ template <int DK, int DV>
 struct Q8Lds {
     __attribute__((aligned(16))) char ring8[2 * NWAVE * Q8Geom<DK>::SLOT];   // [stage][wave] int8 rows + mask
     __attribute__((aligned(16))) char tile[NWAVE * SliceGeom<DK>::STAGE];    // f16 slices; q staging first
-    __attribute__((aligned(16))) half_t px[HG * ShortCfg<DK, DV>::PROW];
+    __attribute__((aligned(16))) half_t px[HG * DecodeCfg<DK, DV>::PROW];
     __attribute__((aligned(16))) float red[2][HG][NWAVE];
-    static_assert(HG * ShortCfg<DK, DV>::OPITCH <= Q8Geom<DK>::SLOT, "the output staging fits a wave's int8 slot");
+    static_assert(HG * DecodeCfg<DK, DV>::OPITCH <= Q8Geom<DK>::SLOT, "the output staging fits a wave's int8 slot");
 };
 
 // DMA of wave w's slice of tile k (clamped into the split) into its int8 slot of stage s: the rows as
@@ -132,7 +132,7 @@ template <int DK, int DV>
 __device__ __forceinline__ void decode_row_q8(const DecodeArgs & a, int t, Q8Lds<DK, DV> & sh) {
     using G = SliceGeom<DK>;
     using G8 = Q8Geom<DK>;
-    using C = ShortCfg<DK, DV>;
+    using C = DecodeCfg<DK, DV>;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
