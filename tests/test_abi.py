@@ -158,6 +158,20 @@ def test_entry_points_reject_before_launching(lib):
     assert lib.mla_m4_phase_merge(None, P(vo), None) == -1
 
 
+def test_q8_prefill_rejects_a_workspace_without_room_for_the_copy(lib):
+    """A workspace that holds the partials but not the 8-bit cache's f16 copy is refused before
+    any launch (the pointer below is never dereferenced: the size check comes first)."""
+    kc = q8((1500,), 576)
+    _, q, mask, out = decode_tensors(n_kv=1500, nt=20)
+    need = A.kqkv_workspace_bytes(kc, q, out)
+    copy = (1500 * 576 * 2 + 255) // 256 * 256
+    P = ctypes.byref
+    vk, vq, vm, vo = ops.view(kc), ops.view(q), ops.view(mask), ops.view(out)
+    fake = ctypes.c_void_p(1 << 20)                               # 16-byte aligned, never used
+    for size in (need - copy, need - 1):
+        assert lib.mla_m4_kqkv(P(vk), P(vq), P(vm), ctypes.c_float(0.1), P(vo), fake, size, None) == -5
+
+
 def test_product_path_has_no_cpu_fallback(monkeypatch, tmp_path):
     """Without the built library every op raises instead of computing anything on the host."""
     monkeypatch.setattr(ops, "_lib", None)
