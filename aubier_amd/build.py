@@ -66,22 +66,6 @@ def build_lib(verbose: bool = True) -> Path:
     return LIB
 
 
-PROBE_SRC = PKG / "probe" / "stream_ceiling.hip"
-PROBE_BIN = PKG / "probe" / "stream_ceiling"
-
-
-def build_probe(verbose: bool = True) -> Path:
-    """The stream-ceiling measurement program (not part of the library; bench.py --ceiling)."""
-    tmp = PROBE_BIN.with_suffix(".tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17",
-          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument",
-          str(PROBE_SRC), "-o", str(tmp)])
-    os.replace(tmp, PROBE_BIN)
-    if verbose:
-        print(f"built {PROBE_BIN.relative_to(ROOT)}")
-    return PROBE_BIN
-
-
 def build_oracle(verbose: bool = True) -> Path:
     cc = shutil.which("gcc") or "cc"
     tmp = ORACLE_LIB.with_suffix(".so.tmp")
@@ -97,15 +81,12 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--lib", action="store_true", help="kernel library only")
     ap.add_argument("--oracle", action="store_true", help="oracle only")
-    ap.add_argument("--probe", action="store_true", help="the stream-ceiling measurement program only")
     args = ap.parse_args(argv)
-    every = not (args.lib or args.oracle or args.probe)
+    every = not (args.lib or args.oracle)
     if args.lib or every:
         build_lib()
     if args.oracle or every:
         build_oracle()
-    if args.probe or every:
-        build_probe()
     return 0
 
 

@@ -135,10 +135,12 @@ __device__ __forceinline__ i32x4 make_rsrc(const void * base, uint32_t num_recor
     return r;
 }
 // 16-byte load through a buffer resource over [base, base + num_records): an offset at or past
-// num_records reads zeros without a memory access -- a per-lane "or zero" with no branch
+// num_records reads zeros without a memory access -- a per-lane "or zero" with no branch.  NT: the
+// non-temporal policy (buffer_load ... nt), for data read once.
+template <bool NT = false>
 __device__ __forceinline__ u32x4 buf_ld16(const void * base, uint32_t num_records, uint32_t off) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)num_records, 0x00020000);
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, NT ? 2 : 0));
 }
 __device__ __forceinline__ uint32_t lds_addr(const void * p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;

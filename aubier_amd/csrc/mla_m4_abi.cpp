@@ -145,19 +145,6 @@ size_t q8_copy_bytes(const KqkvShape & s) {
 
 int64_t n_tiles_of(int64_t n_kv) { return (n_kv + TILE_KEYS - 1) / TILE_KEYS; }
 
-// Single-token decode over an f16 cache (one 32-head group): the step is the partial and then the
-// merge, which reads every split's record (32 heads x D_v f16) back cold, straight after the
-// partial wrote it, so fewer and longer splits can win although the partial alone slows.  From
-// measured steps on the MI355X (WKB + partial + merge, COLD): one tile per split up to 160 tiles,
-// two up to 384, 192 splits up to 768 tiles (32,768 keys: 19.95 us against 20.7-21.2 at 256),
-// then 256.
-int64_t decode_f16_step_splits(int64_t tiles) {
-    if (tiles <= 160) return tiles;
-    if (tiles <= 384) return (tiles + 1) / 2;
-    if (tiles <= 768) return 192;
-    return TARGET_WG;
-}
-
 int default_splits(const KqkvShape & s) {
     // the unit a split is made of: 64-key tiles (MFMA kernels), 16-key granules (VALU kernel)
     const int64_t tiles = (use_mfma(s) || use_q8(s)) ? n_tiles_of(s.n_kv) : (s.n_kv + mla::GRAN_KEYS - 1) / mla::GRAN_KEYS;
@@ -169,8 +156,13 @@ int default_splits(const KqkvShape & s) {
     // when there are few splits), so the split count is the single-row one
     else if (use_mfma(s) || use_q8(s)) groups = (s.n_head + DECODE_HEADS - 1) / DECODE_HEADS;
     else groups = s.n_head * s.nt;
+    // About one workgroup per CU.  For the single-token decode over an f16 cache this is also the
+    // best split count for the whole op (partial, then the merge reading the records back), measured
+    // on the MI355X over 2,048-65,536 keys (WKB + partial + merge, COLD): e.g. 32,768 keys 18.90 us
+    // at 256 splits against 19.32 at 192 and 20.50 at 128; one tile per split below 256 tiles.
+    // (With the records' o read by default-policy loads, which left them in the merge's L2s, fewer
+    // and longer splits had won: 192 at 32,768 keys.)
     int64_t sp = (TARGET_WG + groups - 1) / groups;
-    if (use_mfma(s) && !use_prefill(s) && s.nt == 1 && groups == 1) sp = decode_f16_step_splits(tiles);
     if (sp > tiles) sp = tiles;
     if (sp > MLA_M4_MAX_SPLITS) sp = MLA_M4_MAX_SPLITS;
     if (sp < 1) sp = 1;

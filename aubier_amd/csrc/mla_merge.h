@@ -36,7 +36,12 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
     const char * rec = part_record(part, h / PART_HEADS, nt, t, n_split, dv, (int)sizeof(OT));
     const int cc = min(c, dv - 8);
     // the record's o blocks, read through a buffer resource: an empty split's block (never
-    // written) is skipped by an out-of-range offset, which reads zeros without a memory access
+    // written) is skipped by an out-of-range offset, which reads zeros without a memory access.
+    // Each o line has one reader, so it is loaded non-temporal: records read with the default
+    // policy stay in the readers' L2s, and the next step's partial kernel, rewriting the same
+    // workspace, then ran ~0.65 us longer from its last workgroup to the merge's first loads
+    // (config 3, 192 splits: step 20.0 -> 19.35 us; the (m, l) pairs, read by every column block
+    // of a head, keep the default policy).
     const char * obase = rec + part_o_off(n_split, 0, dv, (int)sizeof(OT));
     const uint32_t oblk = (uint32_t)(PART_HEADS * dv * (int)sizeof(OT));
     const uint32_t orecs = (uint32_t)n_split * oblk;
@@ -58,12 +63,12 @@ __device__ __forceinline__ void merge_unit(const char * __restrict__ part, int d
             // o only where the split has a live key
             const uint32_t off = (ms[j] != -INFINITY) ? (uint32_t)sc_ * oblk + ocol : 0xFFFFFFE0u;   // (+16 stays out of range)
             if constexpr (sizeof(OT) == 2) {
-                const half8 v = __builtin_bit_cast(half8, buf_ld16(obase, orecs, off));
+                const half8 v = __builtin_bit_cast(half8, buf_ld16<true>(obase, orecs, off));
 #pragma unroll
                 for (int k = 0; k < 8; ++k) os[j][k] = (float)v[k];
             } else {
-                const f32x4 v0 = __builtin_bit_cast(f32x4, buf_ld16(obase, orecs, off));
-                const f32x4 v1 = __builtin_bit_cast(f32x4, buf_ld16(obase, orecs, off + 16u));
+                const f32x4 v0 = __builtin_bit_cast(f32x4, buf_ld16<true>(obase, orecs, off));
+                const f32x4 v1 = __builtin_bit_cast(f32x4, buf_ld16<true>(obase, orecs, off + 16u));
 #pragma unroll
                 for (int k = 0; k < 4; ++k) { os[j][k] = v0[k]; os[j][4 + k] = v1[k]; }
             }

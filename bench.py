@@ -83,9 +83,6 @@ def parse():
                          "the CPU baseline and the errors use the f16 values it stands for")
     ap.add_argument("--ops", action="store_true",
                     help="time the reference-geometry quantised ops (Q8_0 WKB, PHASE wv_b, PHASE KV-write) instead")
-    ap.add_argument("--ceiling", action="store_true",
-                    help="run the stream-ceiling probe (config 3's bytes read with no compute; launch cost) "
-                         "and print its figures as one JSON line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="no timing: run the calibration copy and a few steps, for rocprofv3 --pmc")
     return ap.parse_args()
@@ -315,37 +312,12 @@ def decode_record(inp, args, steps, warmup, reps, sweep, cpu_runs, cpu_thr):
     return rec
 
 
-def ceiling(args) -> int:
-    """The stream-ceiling probe (aubier_amd/probe/stream_ceiling.hip), run as a child process before
-    this process touches the GPU: config 3's 37.7 MB read by one launch with no compute, by LDS DMA
-    or into VGPRs, over 256-2,048 workgroups and 1-5 workgroups per CU, and the cost of an empty
-    launch in a graph."""
-    import subprocess
-    exe = ROOT / "aubier_amd" / "probe" / "stream_ceiling"
-    if not exe.exists():
-        print(f"bench.py: {exe.relative_to(ROOT)} is not built (python -m aubier_amd.build --probe)", file=sys.stderr)
-        return 1
-    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True)
-    rows = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
-    if r.returncode != 0 or any("error" in x for x in rows):
-        print(r.stdout, file=sys.stderr)
-        return r.returncode or 1
-    stream = [x for x in rows if x["probe"] == "stream"]
-    best = min(stream, key=lambda x: x["us"] if x["bytes"] > 37e6 else 1e9)
-    print(json.dumps({"metric": "stream ceiling for config 3's bytes (one launch, no compute)", "unit": "us",
-                      "value": best["us"], "best": best, "stream": stream,
-                      "empty_kernel": [x for x in rows if x["probe"] == "empty_kernel"]}), flush=True)
-    return 0
-
-
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the split-K decode path runs on a single "
               "MI355X); multi-GPU runs are not part of it.", file=sys.stderr)
         return 2
-    if args.ceiling:
-        return ceiling(args)
     import torch
     import aubier_amd as A
     from aubier_amd import inputs as I

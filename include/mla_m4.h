@@ -167,10 +167,10 @@ size_t mla_m4_kqkv_workspace_bytes(const mla_m4_tensor * kcache, const mla_m4_te
 int mla_m4_kqkv_noalloc(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
                         const mla_m4_tensor * mask, float kq_scale, const mla_m4_tensor * dst, void * stream);
 
-/* Split count mla_m4_kqkv uses for a decode window of n_kv keys (a function of the window).  For
- * one token over an f16 cache it is chosen for the whole op (partial, then the merge reading the
- * records back): one 64-key tile per split up to 160 tiles, two up to 384, 192 splits up to 768
- * tiles, 256 beyond; otherwise about one workgroup per CU. */
+/* Split count mla_m4_kqkv uses for a decode window of n_kv keys (a function of the window): about
+ * one workgroup per CU, at most one split per 64-key tile (one token over an f16 cache: one tile per
+ * split up to 256 tiles, then 256 splits -- also the fastest choice for the whole op, partial then
+ * merge, measured over 2K-64K keys). */
 int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type);
 
 /* -------------------------------------------------------------------------------------------

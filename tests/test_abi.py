@@ -124,10 +124,11 @@ def test_supports_phase():
 
 
 def test_default_splits_and_workspace(lib):
-    # one token, f16 cache: chosen for the partial + merge step (1 tile per split up to 160 tiles,
-    # 2 up to 384, 192 splits up to 768 tiles, 256 beyond)
-    assert A.default_splits(32768) == 192
-    assert A.default_splits(8192) == 128 and A.default_splits(16384) == 128 and A.default_splits(24576) == 192
+    # one token, f16 cache: about one workgroup per CU, at most one split per 64-key tile (measured
+    # fastest for the partial + merge step as well)
+    assert A.default_splits(32768) == 256
+    assert A.default_splits(8192) == 128 and A.default_splits(16384) == 256 and A.default_splits(24576) == 256
+    assert A.default_splits(12288) == 192 and A.default_splits(4096) == 64
     assert A.default_splits(65536) == 256 and A.default_splits(262144) == 256
     assert A.default_splits(32768, 32, ops.TYPE_Q8_0) == 256                # the 8-bit cache keeps 256
     assert A.default_splits(64) == 1
