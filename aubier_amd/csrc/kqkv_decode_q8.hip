@@ -67,7 +67,9 @@ __device__ __forceinline__ void q8_dma(const SliceStream<DK> & ss, uint32_t ring
     const int tile = min(ss.t0 + min(k, ss.n_my - 1), ss.n_tiles - 1);
     const int key0 = tile * TK + WK * ss.w;
     const int left = ss.n_kv - key0;
-    const i32x4 krs = make_rsrc(ss.kc + (int64_t)key0 * G8::ROWB, left > 0 ? (uint32_t)(left * G8::ROWB) : 0u);
+    // the rows from key0 to the end of the cache: at most the whole cache, which the contract keeps
+    // within 4 GiB (check_kqkv), so the byte count fits the 32-bit range once formed in 64 bits
+    const i32x4 krs = make_rsrc(ss.kc + (int64_t)key0 * G8::ROWB, left > 0 ? (uint32_t)((int64_t)left * G8::ROWB) : 0u);
     const uint32_t sb = ring8 + (uint32_t)((s * NWAVE + ss.w) * G8::SLOT);
 #pragma unroll
     for (int i = 0; i < G8::DMA_FULL; ++i) dma16_nt(krs, 1024u * (uint32_t)i + 16u * (uint32_t)lane, 0u, sb + 1024u * (uint32_t)i);

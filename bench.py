@@ -168,8 +168,10 @@ class Decode:
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            for i in range(2):            # untimed eager warm-up on the capture stream
-                fn((start + i) % self.n_rot)
+            # untimed eager warm-up on the capture stream, on the two copies before `start` (those
+            # a replay from `start` follows anyway), so that the graph's first copy stays COLD
+            for i in range(2):
+                fn((start - 2 + i) % self.n_rot)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
@@ -192,36 +194,43 @@ class Decode:
 
     def run_steps(self, k, warmup, step=None):
         """Exactly `warmup` untimed then exactly `k` timed steps (graphs of glen steps, the
-        remainder as one more graph); returns (us per step, wall seconds of the timed region)."""
+        remainder as one more graph); returns (us per step, wall seconds of the timed region, the
+        rotation index the timed steps start at).  The warm-up starts at rotation index 0 and the
+        timed steps at the index after the warm-up's last, so the first timed step reads a copy
+        last read a whole rotation (> 512 MiB of reads) earlier: every timed step is COLD."""
         torch = self.torch
         step = step or self.step
-        g_full = self.capture(step, self.glen)
-        g_rem = {}
+        w0 = warmup % self.n_rot
+        graphs = {}
 
-        def replay_n(n):
+        def graph(n, start):
+            if (n, start) not in graphs:
+                graphs[(n, start)] = self.capture(step, n, start)
+            return graphs[(n, start)]
+
+        def replay_n(n, start):
+            # a full graph covers whole rotations, so it ends at the index it started at
             for _ in range(n // self.glen):
-                g_full.replay()
-            r = n % self.glen
-            if r:
-                if r not in g_rem:
-                    g_rem[r] = self.capture(step, r)
-                g_rem[r].replay()
+                graph(self.glen, start).replay()
+            if n % self.glen:
+                graph(n % self.glen, start).replay()
 
-        if k % self.glen:
-            g_rem[k % self.glen] = self.capture(step, k % self.glen)
-        if warmup % self.glen and warmup % self.glen not in g_rem:
-            g_rem[warmup % self.glen] = self.capture(step, warmup % self.glen)
+        for n, start in ((warmup, 0), (k, w0)):      # capture everything before the first replay
+            if n >= self.glen:
+                graph(self.glen, start)
+            if n % self.glen:
+                graph(n % self.glen, start)
         torch.cuda.synchronize()
-        replay_n(warmup)
+        replay_n(warmup, 0)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
-        replay_n(k)
+        replay_n(k, w0)
         e1.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        return e0.elapsed_time(e1) * 1000.0 / k, wall
+        return e0.elapsed_time(e1) * 1000.0 / k, wall, w0
 
     def per_kernel(self, reps):
         """Per-launch us of each kernel: graphs of back-to-back launches (COLD)."""
@@ -272,10 +281,11 @@ def cpu_run(inp, threads, runs):
 def decode_timings(d, steps, warmup, reps, sweep):
     """Time one decode configuration: exactly `steps` steps after `warmup`, each kernel, WARM,
     optionally the split sweep, and the dominant kernel's roofline."""
-    us_step, wall = d.run_steps(steps, warmup)
+    us_step, wall, w0 = d.run_steps(steps, warmup)
     k = d.per_kernel(reps)
     r = {"n_kv": d.W, "nt": d.inp.nt, "splits": d.S, "cache": "q8_0" if d.q8 else ("f16" if d.inp.kc_f16 else "f32"),
          "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot, "steps_per_graph": d.glen,
+         "timed_rotation_start": w0,
          "us_step": round(us_step, 3), "wall_s_timed": round(wall, 6),
          "us_wkb": round(k["wkb"], 3), "us_kqkv_partial": round(k["partial"], 3), "us_phase_merge": round(k["merge"], 3),
          "alg_bytes_step": int(d.bytes_step),
@@ -304,6 +314,7 @@ def decode_record(inp, args, steps, warmup, reps, sweep, cpu_runs, cpu_thr):
     if cpu_runs:
         t, ref = cpu_run(inp, cpu_thr, cpu_runs)
         rec["cpu_ms"] = round(t * 1e3, 3)
+        rec["cpu_runs"] = cpu_runs
         rec["cpu_threads"] = cpu_thr
         rec["err_vs_oracle"] = errors(out, ref)
     del d
@@ -376,7 +387,7 @@ def main() -> int:
                 others[str(cfg)] = prefill_record(ic, 48, 8, cpu=not args.no_cpu, cpu_thr=thr["threads"], nested=True)
             else:
                 others[str(cfg)] = decode_record(ic, args, steps=48, warmup=12, reps=4, sweep=False,
-                                                 cpu_runs=0 if args.no_cpu else 3, cpu_thr=thr["threads"])
+                                                 cpu_runs=0 if args.no_cpu else 5, cpu_thr=thr["threads"])
             del ic
         extra["configs"] = others
 
@@ -510,9 +521,9 @@ def prefill_record(inp, steps, warmup, cpu: bool, cpu_thr: int, nested: bool = F
     tf_attn = flop_attn / (us_attn * 1e-6) / 1e12
     cpu_rec, err = None, None
     if cpu:
-        t, ref = cpu_run(inp, cpu_thr, 1)
+        t, ref = cpu_run(inp, cpu_thr, 5)
         cpu_rec = {"value": round(t * 1e6, 1), "unit": "us/step", "cores": cpu_thr, "kind": "port",
-                   "sample": "config 5 full step (WKB + unfused kq/softmax/kqv), one run"}
+                   "sample": "config 5 full step (WKB + unfused kq/softmax/kqv) on the same inputs, median of 5 after 1 warm-up"}
         err = errors(got, ref)
     if nested:
         return {"n_kv": inp.n_kv, "nt": T, "splits": n_split, "cache": "q8_0" if q8 else "f16", "steps": reps * NG, "warmup": warmup,

@@ -177,8 +177,11 @@ int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type
  * Split-K pass 1 on its own: the partial kernel of patches/ggml-m4/m4-kqkv.cu:201-312 with an
  * explicit split count (1 .. MLA_M4_MAX_SPLITS).  Keys are partitioned into n_split contiguous
  * ranges of whole units, balanced (the first n_units % n_split ranges get one more unit): 64-key
- * tiles on the MFMA path (F16 cache, the two instantiated geometries), 16-key granules on the
- * VALU path (F32 cache, other geometries).
+ * tiles on the MFMA path (F16 cache, the two instantiated geometries; a Q8_0 cache), 16-key
+ * granules on the VALU path (F32 cache, other geometries).  With a Q8_0 cache this entry point
+ * always runs the 8-bit decode kernel, one pass over the window per token, also for 16 and more
+ * tokens, where mla_m4_kqkv instead writes the cache's f16 values into its workspace and runs the
+ * chunked-prefill kernel on them: the two agree within the f16-cache bar, not bit for bit.
  *   part F32 ne [MLA_M4_PART_FLOATS(D_v) (F16 cache) or MLA_M4_PART_FLOATS_F32(D_v) (F32 cache),
  *                n_split, nt, ceil(H / 32)] contiguous (layout above);
  *   D_v is the V width the partials are for (512 for the 576-wide cache, 256 for the 320-wide).

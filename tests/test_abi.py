@@ -301,3 +301,31 @@ def test_q8_prefill_workspace_holds_the_f16_copy(dk, dv):
     kc16, q, _, out = decode_tensors(n_kv=1500, nt=15, dk=dk, dv=dv)
     S = A.default_splits(1500, 32, ops.TYPE_Q8_0)   # the 8-bit decode kernel: the single-row count
     assert A.kqkv_workspace_bytes(q8((1500,), dk), q, out) == 15 * S * ops.part_floats(dv, True) * 4
+
+
+def test_q8_cache_size_limit():
+    """The 8-bit cache kernel addresses rows from a tile's first key to the end of the cache through a
+    32-bit buffer range, so the contract keeps the whole Q8_0 cache within 4 GiB: 7,017,920 keys of
+    612 bytes at D_k = 576 are accepted, one more is not (descriptors without data, as in planning)."""
+    lib = A.load_library()
+    P = ctypes.byref
+    n_max = 0xFFFFFFFF // 612
+    assert n_max == 7017920
+
+    def views(n_kv):
+        kc = ops.MlaTensor()
+        kc.type = ops.TYPE_Q8_0
+        for i, (ne, nb) in enumerate([(576, 34), (n_kv, 612), (1, 612 * n_kv), (1, 612 * n_kv)]):
+            kc.ne[i], kc.nb[i] = ne, nb
+        q = ops.view(torch.zeros((1, 32, 576)))
+        out = ops.view(torch.zeros((32, 1, 512)))
+        mask = ops.MlaTensor()
+        mask.type = ops.TYPE_F32
+        for i, (ne, nb) in enumerate([(n_kv, 4), (1, 4 * n_kv), (1, 4 * n_kv), (1, 4 * n_kv)]):
+            mask.ne[i], mask.nb[i] = ne, nb
+        for v in (q, out):
+            v.data = None
+        return kc, q, mask, out
+
+    assert lib.mla_m4_supports_kqkv(*(P(v) for v in views(n_max))) == 1
+    assert lib.mla_m4_supports_kqkv(*(P(v) for v in views(n_max + 1))) == 0

@@ -120,15 +120,17 @@ def test_split_lengths_agree_with_oracle(dev, dk, dv, n_kv, splits, sharp):
             assert mv > 0
         out = run_split(kc_d, q_d, m_d, scale, S, dv)
         outs[S] = out
-        rel = 2e-2 if sharp else 3e-3
+        # sharp bars at ~2x what the MI355X measured on these inputs: max_rel vs the oracle <= 4.97e-4
+        # (576/512) / 4.81e-4 (320/256), vs float64 <= 1.93e-3 / 1.07e-3
+        rel = 1e-3 if sharp else 3e-3
         check(f"{dk}/{dv} n_kv={n_kv} S={S} ({tps} tiles/split) sharp={sharp} vs oracle", out, ref, 1e-2, rel)
-        check(f"{dk}/{dv} S={S} sharp={sharp} vs f64 (heads 0-3)", out[:4], ref64, 1e-2, 1e-2 if sharp else 1e-3)
+        check(f"{dk}/{dv} S={S} sharp={sharp} vs f64 (heads 0-3)", out[:4], ref64, 1e-2, 4e-3 if sharp else 1e-3)
     # the split counts against each other on the same inputs
     ss = sorted(outs)
     for a_, b_ in zip(ss, ss[1:]):
         ea, er, _ = errs(outs[a_], outs[b_])
         say(f"S={a_} vs S={b_}: max_abs={ea:.3e} max_rel={er:.3e}")
-        assert ea <= 1e-2 and er <= (2e-2 if sharp else 3e-3)
+        assert ea <= 1e-2 and er <= 1.5e-3      # measured <= 6.2e-4, sharp or not
 
 
 @pytest.mark.parametrize("dk,dv,n_kv,nt,splits", [

@@ -108,12 +108,14 @@ def test_q8_cache_cases(dev, dk, dv, n_kv, nt, splits, holes, q_scale):
     ref = orc.kqkv(deq, q, mask, SCALE, d_v=dv)
     ref64 = orc.attn_f64(deq, q[:, :4], mask, SCALE, d_v=dv)
     q_d, m_d = torch.from_numpy(q).to(dev), torch.from_numpy(mask).to(dev)
-    rel = 2e-2 if q_scale > 1 else 3e-3
+    # sharp (q_scale 300) bars at ~2x the MI355X's measured errors: max_rel vs the oracle <= 4.45e-4,
+    # vs float64 <= 1.45e-3
+    rel = 1e-3 if q_scale > 1 else 3e-3
     for S in splits:
         out = run(kq, q_d, m_d, S, dv)
         tag = f"q8 {dk}/{dv} n_kv={n_kv} nt={nt} S={S} q_scale={q_scale}"
         check(f"{tag} vs oracle(dequantised)", out, ref, 1e-2, rel)
-        check(f"{tag} vs f64(dequantised), heads 0-3", out[:4], ref64, 1e-2, 1e-2 if q_scale > 1 else 1e-3)
+        check(f"{tag} vs f64(dequantised), heads 0-3", out[:4], ref64, 1e-2, 3e-3 if q_scale > 1 else 1e-3)
     if q_scale <= 1:
         eq, _, _ = errs(ref, orc.kqkv(kc, q, mask, SCALE, d_v=dv))
         bound, ds = quant_bound(kc, deq, q, dv)
@@ -176,9 +178,11 @@ def test_q8_cache_chunked_prefill(dev, dk, dv):
     check(f"q8 chunked prefill {dk}/{dv} nt=20 vs oracle(dequantised)", out, ref, 1e-2, 3e-3)
     via_f16 = run(torch.from_numpy(deq).to(dev), q_d, m_d, None, dv)
     assert np.array_equal(out, via_f16)
-    # the explicit-split entry point keeps the per-token 8-bit kernel: same bars
+    # the explicit-split entry point keeps the per-token 8-bit kernel (include/mla_m4.h says so):
+    # the same bars against the oracle, and against the op's f16-copy path on the same operands
     out_p = run(kq, q_d, m_d, 7, dv)
     check(f"q8 chunked prefill {dk}/{dv} nt=20 S=7 (8-bit kernel) vs oracle(dequantised)", out_p, ref, 1e-2, 3e-3)
+    check(f"q8 chunked prefill {dk}/{dv} nt=20 S=7 (8-bit kernel) vs mla_m4_kqkv (f16 copy)", out_p, out, 1e-2, 3e-3)
 
 
 def test_q8_cache_prefill_config5_shape(dev):

@@ -81,3 +81,32 @@ def test_noalloc_rejects_partials_beyond_scratch(dev):
     ws = A.ggml_m4_kqkv(g["kcache"], g["qcur"], g["mask"], inp.kq_scale)
     torch.cuda.synchronize()
     assert torch.equal(got, ws)
+
+
+def test_noalloc_under_graph_capture(dev):
+    """The callers the entry point is for: code under hipGraph capture.  One eager call first (it
+    resolves the scratch array's address on this device), then the call captured with
+    capture_error_mode="global" (an allocation, synchronisation or host read inside it would fail
+    the capture).  Three replays, each after new q values are copied into the captured buffer and
+    followed by eager work and a synchronisation, must each be bit-identical to mla_m4_kqkv (with
+    its own workspace) on the same operands."""
+    inp, g = _inputs(dev, 3, 32768, 1)
+    out = torch.empty((I.N_HEAD, 1, I.D_V), dtype=torch.float32, device=dev)
+    A.ggml_m4_kqkv_noalloc(g["kcache"], g["qcur"], g["mask"], inp.kq_scale, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="global"):
+        A.ggml_m4_kqkv_noalloc(g["kcache"], g["qcur"], g["mask"], inp.kq_scale, out=out)
+    for rep in range(3):
+        qn = I.randn(9300 + rep, 32 * I.D_K, 0.05).reshape(1, 32, I.D_K)
+        g["qcur"].copy_(torch.from_numpy(qn).to(dev))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ws = A.ggml_m4_kqkv(g["kcache"], g["qcur"], g["mask"], inp.kq_scale)
+        torch.cuda.synchronize()
+        got, ref = out.cpu().numpy(), ws.cpu().numpy()
+        nbad = int(np.count_nonzero(got.view(np.uint32) != ref.view(np.uint32)))
+        say(f"noalloc graph replay {rep}: {nbad} differing words of {got.size}")
+        assert np.isfinite(got).all() and nbad == 0
