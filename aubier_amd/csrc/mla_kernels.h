@@ -78,6 +78,28 @@ hipError_t launch_q8_rows_to_f16(int dk, const char * src, int n_kv, void * dst,
 constexpr int GRAN_KEYS = 16;
 hipError_t launch_kqkv_generic(int dk, int dv, int kc_is_f16, const DecodeArgs & a, hipStream_t stream);
 
+// Short decode windows in one launch (kqkv_flat.hip): one workgroup per (split of <= FLAT_KEYS keys,
+// head) of one token; each writes a record (m, l, unnormalised o: dv + 4 floats) to rec
+// [head][split], and the last workgroup of each head (an agent-scope ticket per head, ticket[h],
+// zero before the launch and left zero after it) merges the head's records into dst.
+constexpr int FLAT_KEYS = 32;
+constexpr int FLAT_DK_MAX = 576;
+constexpr int FLAT_ROW_PITCH = FLAT_DK_MAX * 4 + 128;    // LDS row pitch: 128 mod 256, distinct banks
+constexpr int FLAT_MAX_SPLITS = 16;                      // windows up to 512 keys
+struct FlatArgs {
+    const char * kc;        // cache base (f32 or f16 rows)
+    int64_t kc_nb1;
+    const float * q;        // token 0's q, head h at q + h * q_nb1 bytes
+    int64_t q_nb1;
+    const float * mask;     // token 0's mask row, or null
+    float scale_log2;       // kq_scale * log2(e)
+    int n_kv, n_head, n_split, dk, dv;
+    float * rec;            // n_head * n_split * (dv + 4) floats
+    unsigned * ticket;      // n_head counters
+    float * dst;            // [H][dv]
+};
+hipError_t launch_kqkv_flat(int kc_is_f16, const FlatArgs & a, hipStream_t stream);
+
 // Split-K merge: partial blocks [group][token][split] (o of o_bytes = 2 or 4) -> dst [dv, nt, H]
 hipError_t launch_merge(const char * part, int dv, int o_bytes, int n_split, int nt, int n_head, float * dst,
                         hipStream_t stream);

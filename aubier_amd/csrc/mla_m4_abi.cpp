@@ -348,15 +348,97 @@ void * scratch_ptr() {
     return g_scratch_ptr[dev];
 }
 
+// ---------------------------------------------------------------- one-launch short windows
+// One decode token over a short window runs kqkv_flat.hip's kernel: splits of <= 32 keys, the merge
+// by the last workgroup of each head, one launch.  Measured on the MI355X (WKB + KQKV, COLD, 32
+// heads, D_k 576): F32 cache 64 / 256 / 512 keys 9.85 / 11.46 / 15.10 us against 14.11 / 14.40 /
+// 15.50 us for split-K partial + merge; F16 cache 64 / 256 keys 10.37 / 11.51 us against
+// 12.73 / 13.18 us, but 512 keys 14.78 against 13.46 (every head's workgroups re-read the split's
+// rows, and the MFMA kernel reads them once), hence the F16 bound.
+constexpr int FLAT_MAX_HEADS = 256;
+constexpr int FLAT_F16_MAX_KEYS = 256;
+bool flat_eligible(const KqkvShape & s) {
+    if (s.nt != 1 || (s.kc_type != MLA_M4_TYPE_F32 && s.kc_type != MLA_M4_TYPE_F16)) return false;
+    const bool f16 = s.kc_type == MLA_M4_TYPE_F16;
+    const int64_t es = f16 ? 2 : 4;
+    const int64_t max_keys = f16 ? FLAT_F16_MAX_KEYS : (int64_t)mla::FLAT_KEYS * mla::FLAT_MAX_SPLITS;
+    return s.n_kv <= max_keys && s.dk <= mla::FLAT_DK_MAX && s.dk % (16 / es) == 0 && s.dv <= 512 && s.dv % 2 == 0 &&
+           s.n_head <= FLAT_MAX_HEADS;
+}
+int flat_splits(const KqkvShape & s) { return (int)((s.n_kv + mla::FLAT_KEYS - 1) / mla::FLAT_KEYS); }
+size_t flat_bytes(const KqkvShape & s) { return (size_t)s.n_head * (size_t)flat_splits(s) * (size_t)(s.dv + 4) * 4u; }
+
+// The flat kernel's per-head tickets: a static device array, zero when the library loads; every
+// launch leaves its tickets zero again.  Launches that overlap on one GPU must not share tickets,
+// so each (device, stream) pair gets a slot of its own on its first call, kept for the process
+// (FLAT_SLOTS pairs; past that, a new stream takes the split-K path).  As with the scratch array,
+// host code uses only the address hipGetSymbolAddress returns for the current device.
+constexpr int FLAT_SLOTS = 32;
+static __device__ __align__(256) unsigned flat_tickets[FLAT_SLOTS * FLAT_MAX_HEADS];
+struct FlatSlot {
+    int dev;
+    hipStream_t st;
+};
+std::mutex g_flat_mu;
+FlatSlot g_flat_slot[FLAT_SLOTS];
+int g_flat_n = 0;
+unsigned * g_flat_base[MAX_DEVICES] = {};
+
+unsigned * flat_ticket_slot(hipStream_t st) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(g_flat_mu);
+    if (g_flat_base[dev] == nullptr) {
+        void * p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(flat_tickets)) != hipSuccess || p == nullptr) return nullptr;
+        g_flat_base[dev] = static_cast<unsigned *>(p);
+    }
+    for (int i = 0; i < g_flat_n; ++i)
+        if (g_flat_slot[i].dev == dev && g_flat_slot[i].st == st) return g_flat_base[dev] + (size_t)i * FLAT_MAX_HEADS;
+    if (g_flat_n == FLAT_SLOTS) return nullptr;
+    g_flat_slot[g_flat_n] = FlatSlot{dev, st};
+    return g_flat_base[dev] + (size_t)(g_flat_n++) * FLAT_MAX_HEADS;
+}
+
+int flat_launch(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask, float kq_scale,
+                const mla_m4_tensor * dst, const KqkvShape & s, char * work, unsigned * tickets, hipStream_t st) {
+    mla::FlatArgs a{};
+    a.kc = static_cast<const char *>(kcache->data);
+    a.kc_nb1 = (int64_t)kcache->nb[1];
+    a.q = static_cast<const float *>(q->data);
+    a.q_nb1 = (int64_t)q->nb[1];
+    a.mask = s.has_mask ? static_cast<const float *>(mask->data) : nullptr;
+    a.scale_log2 = kq_scale * 1.4426950408889634f;
+    a.n_kv = (int)s.n_kv;
+    a.n_head = (int)s.n_head;
+    a.n_split = flat_splits(s);
+    a.dk = (int)s.dk;
+    a.dv = (int)s.dv;
+    a.rec = reinterpret_cast<float *>(work);
+    a.ticket = tickets;
+    a.dst = static_cast<float *>(dst->data);
+    return mla::launch_kqkv_flat(s.kc_type == MLA_M4_TYPE_F16, a, st) == hipSuccess ? MLA_M4_OK : MLA_M4_ERR_LAUNCH;
+}
+
 // Workspace bytes of mla_m4_kqkv at split count sp: the f16 copy of an 8-bit cache for chunked
-// prefill, then the split-K partials.
-size_t kqkv_work_bytes(const KqkvShape & s, int sp) { return q8_copy_bytes(s) + (sp > 1 ? part_bytes(s, sp) : 0); }
+// prefill, then the split-K partials; a short window needs room for the flat kernel's records too
+// (or its split-K fallback).
+size_t kqkv_work_bytes(const KqkvShape & s, int sp) {
+    const size_t split_k = q8_copy_bytes(s) + (sp > 1 ? part_bytes(s, sp) : 0);
+    if (!flat_eligible(s)) return split_k;
+    const size_t flat = flat_bytes(s);
+    return flat > split_k ? flat : split_k;
+}
 
 // The KQKV launch sequence shared by mla_m4_kqkv and mla_m4_kqkv_noalloc, over `work` (>=
 // kqkv_work_bytes(s, sp)): for chunked prefill over an 8-bit cache, its f16 copy first; then with
 // one split the attention kernel writes dst, otherwise partials and the merge.
 int kqkv_launch(const mla_m4_tensor * kcache, const mla_m4_tensor * q, const mla_m4_tensor * mask, float kq_scale,
                 const mla_m4_tensor * dst, const KqkvShape & s, int sp, char * work, hipStream_t st) {
+    if (flat_eligible(s)) {
+        unsigned * tickets = flat_ticket_slot(st);
+        if (tickets != nullptr) return flat_launch(kcache, q, mask, kq_scale, dst, s, work, tickets, st);
+    }
     mla::DecodeArgs a = make_args(kcache, q, mask, kq_scale, s, sp);
     const bool f16_copy = use_q8_prefill(s);
     if (f16_copy) {

@@ -140,6 +140,11 @@ class Decode:
                                             (A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32))
         self.part = self.new_part(self.S)
         self.out = torch.empty((H, inp.nt, DV), dtype=torch.float32, device=dev)
+        # the op's own workspace (what the glue takes from the ggml pool)
+        need = A.kqkv_workspace_bytes(self.kcs[0], self.qcurs[0], self.out)
+        self.ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        # a short window runs as one launch (kqkv_flat.hip), longer ones as partial + merge
+        self.flat = inp.nt == 1 and not self.q8 and inp.n_kv <= (256 if inp.kc_f16 else 512)
         torch.cuda.synchronize()
 
     def new_part(self, S):
@@ -156,11 +161,15 @@ class Decode:
     def merge(self, part=None):
         self.A.ggml_m4_phase_merge(part if part is not None else self.part, out=self.out, n_head=self.H, d_v=self.DV)
 
+    def kqkv(self, i):
+        """GGML_OP_M4_KQKV as the engine's glue calls it, with its workspace: the split-K partial
+        kernel, then the PHASE merge (or, for a short window, the one-launch kernel)."""
+        self.A.ggml_m4_kqkv(self.kcs[i], self.qcurs[i], self.mask, self.inp.kq_scale, out=self.out, workspace=self.ws)
+
     def step(self, i):
-        """WKB -> KQKV pass 1 -> PHASE merge (what GGML_OP_M4_KQKV launches with its workspace)."""
+        """WKB -> KQKV."""
         self.wkb(i)
-        self.attn(i)
-        self.merge()
+        self.kqkv(i)
 
     def capture(self, fn, n, start=0):
         torch = self.torch
@@ -236,6 +245,7 @@ class Decode:
         """Per-launch us of each kernel: graphs of back-to-back launches (COLD)."""
         n = self.glen
         return {"wkb": self.time_graph(self.capture(self.wkb, n), reps, n),
+                "kqkv": self.time_graph(self.capture(self.kqkv, n), reps, n),
                 "partial": self.time_graph(self.capture(self.attn, n), reps, n),
                 "merge": self.time_graph(self.capture(lambda i: self.merge(), n), reps, n)}
 
@@ -287,7 +297,9 @@ def decode_timings(d, steps, warmup, reps, sweep):
          "steps": steps, "warmup": warmup, "rotating_copies": d.n_rot, "steps_per_graph": d.glen,
          "timed_rotation_start": w0,
          "us_step": round(us_step, 3), "wall_s_timed": round(wall, 6),
-         "us_wkb": round(k["wkb"], 3), "us_kqkv_partial": round(k["partial"], 3), "us_phase_merge": round(k["merge"], 3),
+         "us_wkb": round(k["wkb"], 3), "us_kqkv_op": round(k["kqkv"], 3),
+         "kqkv_path": "one launch (flat kernel, in-kernel merge)" if d.flat else "split-K partial + PHASE merge",
+         "us_kqkv_partial": round(k["partial"], 3), "us_phase_merge": round(k["merge"], 3),
          "alg_bytes_step": int(d.bytes_step),
          "cache_bytes_per_key": (d.DK // 32 * 34 if d.q8 else d.DK * d.es) + 4,     # cache row + mask
          "step_GBps": round(d.bytes_step / (us_step * 1e3), 1),

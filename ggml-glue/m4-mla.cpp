@@ -70,7 +70,8 @@ void ggml_cuda_m4_kqkv(ggml_backend_cuda_context & ctx, ggml_tensor * dst) {
     // The split-K partials come from the context's pool, like every other temporary of this
     // backend: ggml captures its graphs in relaxed mode after uncaptured warm-up evaluations, and
     // the pool keeps (and re-hands) the memory a captured node was given.  Decode at 32 heads and
-    // an F16 cache needs 8.45 MB per token (256 splits); one token of a short window needs none.
+    // an F16 cache needs 8.45 MB per token (256 splits); one token of a short window (one launch)
+    // needs D_v + 4 floats per head and 32-key split, 528 KB at 32 heads and 256 keys.
     const size_t need = mla_m4_kqkv_workspace_bytes(&k, &q, &o);
     ggml_cuda_pool_alloc<char> ws(ctx.pool());
     if (need > 0) {

@@ -134,9 +134,15 @@ int mla_m4_wkb(const mla_m4_tensor * w, const mla_m4_tensor * q_nope,
  * score minus a running reference max, at most 2^15) -- ggml-cpu rounds the normalised P instead,
  * which is subnormal in f16 at long context, so results differ from the oracle by more than one
  * rounding there (and are closer to exact arithmetic); an F32 cache runs in f32.
- * Up to 15 tokens (nt) run the decode kernels, split-K (partial + merge, two launches); from 16
- * tokens the prefill kernel (4 tokens per workgroup sharing each K/V tile).
- * `workspace` (device memory, >= mla_m4_kqkv_workspace_bytes()) holds the split-K partials, and,
+ * One token over a short window (an F32 cache of at most 512 keys, an F16 cache of at most 256,
+ * D_k <= 576) runs in one launch: splits of at most 32 keys, one workgroup per (split, head), and
+ * the last workgroup of each head (a ticket counter per head) merges the head's splits into dst.
+ * Its tickets live in a static device array with one slot per (device, stream) -- 32 such pairs
+ * per process; a stream beyond them takes the split-K path.  Otherwise up to 15 tokens (nt) run
+ * the decode kernels, split-K (partial + merge, two launches); from 16 tokens the prefill kernel
+ * (4 tokens per workgroup sharing each K/V tile).
+ * `workspace` (device memory, >= mla_m4_kqkv_workspace_bytes()) holds the split-K partials (or the
+ * one-launch kernel's per-split records: (m, l, o) in D_v + 4 floats per head and split), and,
  * for 16 or more tokens over a Q8_0 cache, first the cache's f16 values (n_kv x D_k x 2 bytes,
  * rounded up to 256), which the f16 prefill kernel then reads (a third launch before it).
  * ------------------------------------------------------------------------------------------- */

@@ -138,8 +138,20 @@ def test_default_splits_and_workspace(lib):
     kc, q, _, out = decode_tensors(n_kv=32768)
     S = A.default_splits(32768)
     assert A.kqkv_workspace_bytes(kc, q, out) == S * ops.part_floats(512) * 4
+    # a short window (one token, an f16 cache of <= 256 keys or an f32 one of <= 512) runs the
+    # one-launch kernel: records of (m, l, o) per (head, split of <= 32 keys), D_v + 4 floats each
     kc, q, _, out = decode_tensors(n_kv=64)
-    assert A.kqkv_workspace_bytes(kc, q, out) == 0                 # one split: no partials
+    assert A.kqkv_workspace_bytes(kc, q, out) == 32 * 2 * (512 + 4) * 4
+    kc, q, _, out = decode_tensors(n_kv=256)
+    assert A.kqkv_workspace_bytes(kc, q, out) == max(32 * 8 * (512 + 4) * 4, A.default_splits(256) * ops.part_floats(512) * 4)
+    kc, q, _, out = decode_tensors(n_kv=512, dtype=torch.float32)
+    assert A.kqkv_workspace_bytes(kc, q, out) == max(32 * 16 * (512 + 4) * 4, A.default_splits(512) * ops.part_floats(512) * 4)
+    kc, q, _, out = decode_tensors(n_kv=512)                      # f16 at 512 keys: split-K
+    assert A.kqkv_workspace_bytes(kc, q, out) == A.default_splits(512) * ops.part_floats(512) * 4
+    # a long single-split decode needs none
+    kc, q, _, out = decode_tensors(n_kv=64, dtype=torch.float16)
+    q2 = torch.zeros((2, 32, 576))
+    assert A.kqkv_workspace_bytes(kc, q2, torch.zeros((32, 2, 512))) == 0      # two tokens, one tile: one split
 
 
 def test_entry_points_reject_before_launching(lib):
