@@ -5,14 +5,16 @@ achieved HBM GB/s as a fraction of peak, at 32,768 keys).
 
 One step = the MLA attention of one decode token, as the engine's layer graph runs it:
 GGML_OP_M4_WKB (absorbed q_nope written into the Qcur buffer) -> GGML_OP_M4_KQKV (the split-K
-partial kernel, then the PHASE merge kernel), through the C ABI, on seeded synthetic inputs
+partial kernel, then the PHASE merge kernel; for a short window, one launch that merges its own
+splits), through the C ABI, on seeded synthetic inputs
 (aubier_amd.inputs).  The steps are captured in hipGraphs (the way the engine runs them) and
 replayed; consecutive steps read different copies of the KV cache and W_kb (enough copies that
 a full rotation exceeds 512 MiB, twice the 256 MB MALL), so every step streams from HBM (COLD).
 Exactly K steps are timed (whole rotations plus one graph of the remainder), after exactly W
 untimed warm-up steps.
 
-Prints ONE JSON line.  `roofline` is for the dominant kernel (the split-K partial): algorithmic
+Prints ONE JSON line.  `roofline` is for the dominant kernel (the split-K partial, or the
+one-launch kernel of a short window, timed as the whole op): algorithmic
 bytes per launch (n_kv * (1152 cache + 4 mask) + Qcur) / its average duration, timed with HIP
 events around a graph of back-to-back launches on the stream they run on.  `cpu_baseline` is the
 CPU oracle (the restated unfused ggml graph) on the host threads this process may use, same
@@ -83,6 +85,8 @@ def parse():
                          "the CPU baseline and the errors use the f16 values it stands for")
     ap.add_argument("--ops", action="store_true",
                     help="time the reference-geometry quantised ops (Q8_0 WKB, PHASE wv_b, PHASE KV-write) instead")
+    ap.add_argument("--layer", action="store_true",
+                    help="us per attention layer (KV-write -> WKB -> concat -> KQKV -> wv_b), both geometries")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="no timing: run the calibration copy and a few steps, for rocprofv3 --pmc")
     return ap.parse_args()
@@ -96,7 +100,83 @@ def errors(out: np.ndarray, ref: np.ndarray) -> dict:
             "rms_rel": float(np.sqrt((d ** 2).mean()) / scale)}
 
 
-class Decode:
+class Rotated:
+    """Graph capture and timing over rotating input copies (COLD): a subclass sets torch, n_rot
+    (copies, one rotation > COLD_BYTES of reads), glen (steps per graph, whole rotations) and
+    step(i) (one step on copy i)."""
+
+    def capture(self, fn, n, start=0):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            # untimed eager warm-up on the capture stream, on the two copies before `start` (those
+            # a replay from `start` follows anyway), so that the graph's first copy stays COLD
+            for i in range(2):
+                fn((start - 2 + i) % self.n_rot)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn((start + i) % self.n_rot)
+        return g
+
+    def time_graph(self, g, reps, per):
+        """us per unit: replay g `reps` times (each replay = `per` units) between two events."""
+        torch = self.torch
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (reps * per)
+
+    def run_steps(self, k, warmup, step=None):
+        """Exactly `warmup` untimed then exactly `k` timed steps (graphs of glen steps, the
+        remainder as one more graph); returns (us per step, wall seconds of the timed region, the
+        rotation index the timed steps start at).  The warm-up starts at rotation index 0 and the
+        timed steps at the index after the warm-up's last, so the first timed step reads a copy
+        last read a whole rotation (> 512 MiB of reads) earlier: every timed step is COLD."""
+        torch = self.torch
+        step = step or self.step
+        w0 = warmup % self.n_rot
+        graphs = {}
+
+        def graph(n, start):
+            if (n, start) not in graphs:
+                graphs[(n, start)] = self.capture(step, n, start)
+            return graphs[(n, start)]
+
+        def replay_n(n, start):
+            # a full graph covers whole rotations, so it ends at the index it started at
+            for _ in range(n // self.glen):
+                graph(self.glen, start).replay()
+            if n % self.glen:
+                graph(n % self.glen, start).replay()
+
+        for n, start in ((warmup, 0), (k, w0)):      # capture everything before the first replay
+            if n >= self.glen:
+                graph(self.glen, start)
+            if n % self.glen:
+                graph(n % self.glen, start)
+        torch.cuda.synchronize()
+        replay_n(warmup, 0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        replay_n(k, w0)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return e0.elapsed_time(e1) * 1000.0 / k, wall, w0
+
+
+class Decode(Rotated):
     """Device buffers and launch closures of one decode configuration (nt rows, W keys)."""
 
     def __init__(self, inp, splits: int = 0):
@@ -171,76 +251,6 @@ class Decode:
         self.wkb(i)
         self.kqkv(i)
 
-    def capture(self, fn, n, start=0):
-        torch = self.torch
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            # untimed eager warm-up on the capture stream, on the two copies before `start` (those
-            # a replay from `start` follows anyway), so that the graph's first copy stays COLD
-            for i in range(2):
-                fn((start - 2 + i) % self.n_rot)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g):
-            for i in range(n):
-                fn((start + i) % self.n_rot)
-        return g
-
-    def time_graph(self, g, reps, per):
-        """us per unit: replay g `reps` times (each replay = `per` units) between two events."""
-        torch = self.torch
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1000.0 / (reps * per)
-
-    def run_steps(self, k, warmup, step=None):
-        """Exactly `warmup` untimed then exactly `k` timed steps (graphs of glen steps, the
-        remainder as one more graph); returns (us per step, wall seconds of the timed region, the
-        rotation index the timed steps start at).  The warm-up starts at rotation index 0 and the
-        timed steps at the index after the warm-up's last, so the first timed step reads a copy
-        last read a whole rotation (> 512 MiB of reads) earlier: every timed step is COLD."""
-        torch = self.torch
-        step = step or self.step
-        w0 = warmup % self.n_rot
-        graphs = {}
-
-        def graph(n, start):
-            if (n, start) not in graphs:
-                graphs[(n, start)] = self.capture(step, n, start)
-            return graphs[(n, start)]
-
-        def replay_n(n, start):
-            # a full graph covers whole rotations, so it ends at the index it started at
-            for _ in range(n // self.glen):
-                graph(self.glen, start).replay()
-            if n % self.glen:
-                graph(n % self.glen, start).replay()
-
-        for n, start in ((warmup, 0), (k, w0)):      # capture everything before the first replay
-            if n >= self.glen:
-                graph(self.glen, start)
-            if n % self.glen:
-                graph(n % self.glen, start)
-        torch.cuda.synchronize()
-        replay_n(warmup, 0)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record()
-        replay_n(k, w0)
-        e1.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        return e0.elapsed_time(e1) * 1000.0 / k, wall, w0
-
     def per_kernel(self, reps):
         """Per-launch us of each kernel: graphs of back-to-back launches (COLD)."""
         n = self.glen
@@ -271,6 +281,151 @@ class Decode:
         self.step(0)
         self.torch.cuda.synchronize()
         return self.out.cpu().numpy()
+
+
+class Layer(Rotated):
+    """One attention layer of a decode step (one token), as the engine's captured layer graph runs
+    it (engine/m1_layer.cpp:411-442 builds the chain; engine/m1_session.h:155-158 prices the M4 ops per
+    layer in situ), COLD: the cache and every weight rotate over copies.
+      geometry "ref" -- the reference engine's: KV row 320 (256 latent + 64 rope), Q8_0 W_kb
+        [64,256,32], Q8_0 wkv_a [4096,320] and wv_b [256,128,32]:
+        PHASE KV-write -> WKB -> concat (the rope half into Qcur) -> KQKV -> PHASE wv_b;
+      geometry "baseline" -- BASELINE.json's: KV row 576, f32 W_kb [128,512,32]: WKB -> KQKV.
+    The new token's row is written at position n_kv - 1 and every key is live."""
+
+    GEOM = {"ref": dict(d_n=64, d_r=64, d_lat=256, n_embd=4096, d_out=128),
+            "baseline": dict(d_n=128, d_r=64, d_lat=512)}
+    ROPE = dict(freq_base=1e6, freq_scale=0.25, ext_factor=1.0, attn_factor=1.0, beta_fast=32.0, beta_slow=1.0,
+                eps=1e-6, n_ctx_orig=8192)
+
+    def __init__(self, geom: str, n_kv: int, seed: int = 9600):
+        import torch
+        import aubier_amd as A
+        self.torch, self.A, self.geom, self.W = torch, A, geom, n_kv
+        g = self.GEOM[geom]
+        H = self.H = 32
+        d_n, d_r, d_lat = self.d_n, self.d_r, self.d_lat = g["d_n"], g["d_r"], g["d_lat"]
+        dk = d_lat + d_r
+        self.full = geom == "ref"
+        dev = torch.device("cuda:0")
+        rng = np.random.default_rng(seed)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+
+        def q8_blocks(rows, ne0):
+            nb = ne0 // 32
+            b = np.empty((rows, nb, 34), dtype=np.uint8)
+            b[:, :, :2] = (np.abs(rng.standard_normal((rows, nb))) * 0.01 + 0.001).astype(np.float16) \
+                .view(np.uint8).reshape(rows, nb, 2)
+            b[:, :, 2:] = rng.integers(-127, 128, size=(rows, nb, 32)).astype(np.int8).view(np.uint8)
+            return torch.from_numpy(b.reshape(rows, nb * 34)).to(dev)
+
+        # bytes each step reads or writes, op by op (weights, activations, outputs, the cache)
+        kc_bytes = n_kv * dk * 2
+        by = {"wkb": (H * d_lat * d_n // 32 * 34 if self.full else H * d_lat * d_n * 4) + H * d_n * 4 + H * d_lat * 4,
+              "kqkv": kc_bytes + n_kv * 4 + H * dk * 4 + H * d_lat * 4}
+        if self.full:
+            n_embd, d_out = g["n_embd"], g["d_out"]
+            by["kvwrite"] = dk * n_embd // 32 * 34 + n_embd * 4 + d_lat * 4 + dk * 4 + dk * 2
+            by["concat"] = 2 * H * d_r * 4
+            by["wvb"] = H * d_out * d_lat // 32 * 34 + H * d_lat * 4 + H * d_out * 4
+        self.bytes = by
+        rot_bytes = kc_bytes + by["wkb"] + by.get("kvwrite", 0) + by.get("wvb", 0)
+        self.n_rot = max(12, math.ceil(COLD_BYTES / rot_bytes))
+        self.glen = self.n_rot * math.ceil(GRAPH_MIN_STEPS / self.n_rot)
+        R = self.n_rot
+
+        kc0 = (torch.randn((n_kv, dk), generator=gen, device=dev) * 0.05).to(torch.float16)
+        self.kcs = [kc0] + [kc0.clone() for _ in range(R - 1)]
+        q0 = torch.randn((1, H, d_n + d_r), generator=gen, device=dev) * 0.05
+        self.qs = [q0] + [q0.clone() for _ in range(R - 1)]
+        if self.full:
+            w = q8_blocks(H * d_lat, d_n).view(H, d_lat, d_n // 32 * 34)
+            self.wkbs = [A.Q8_0(x, d_n) for x in [w] + [w.clone() for _ in range(R - 1)]]
+            w = q8_blocks(dk, n_embd)
+            self.wkvas = [A.Q8_0(x, n_embd) for x in [w] + [w.clone() for _ in range(R - 1)]]
+            w = q8_blocks(H * d_out, d_lat).view(H, d_out, d_lat // 32 * 34)
+            self.wvbs = [A.Q8_0(x, d_lat) for x in [w] + [w.clone() for _ in range(R - 1)]]
+            c0 = torch.randn(n_embd, generator=gen, device=dev)
+            self.curs = [c0] + [c0.clone() for _ in range(R - 1)]
+            self.nw = (1.0 + 0.25 * torch.randn(d_lat, generator=gen, device=dev)).contiguous()
+            self.kidx = torch.tensor([n_kv - 1], dtype=torch.int64, device=dev)
+            self.pos = torch.tensor([n_kv - 1], dtype=torch.int32, device=dev)
+            self.rope = A.rope_params(n_dims=d_r, **self.ROPE)
+            self.kcur = torch.empty(dk, dtype=torch.float32, device=dev)
+            self.out = torch.empty((H, 1, d_out), dtype=torch.float32, device=dev)
+        else:
+            w = torch.randn((H, d_lat, d_n), generator=gen, device=dev) * 0.05
+            self.wkbs = [w] + [w.clone() for _ in range(R - 1)]
+        self.qcur = torch.zeros((1, H, dk), dtype=torch.float32, device=dev)
+        if not self.full:                       # no concat in this chain: the rope half is set once
+            self.qcur[:, :, d_lat:] = q0[:, :, d_n:]
+        self.mask = torch.zeros((1, n_kv), dtype=torch.float32, device=dev)
+        self.kqv = torch.empty((H, 1, d_lat), dtype=torch.float32, device=dev)
+        self.kq_scale = 1.0 / math.sqrt(d_n + d_r)
+        need = A.kqkv_workspace_bytes(self.kcs[0], self.qcur, self.kqv)
+        self.ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        self.ops = {"wkb": self.wkb, "kqkv": self.kqkv}
+        if self.full:
+            self.ops = {"kvwrite": self.kvwrite, "wkb": self.wkb, "concat": self.concat, "kqkv": self.kqkv,
+                        "wvb": self.wvb}
+        torch.cuda.synchronize()
+
+    def kvwrite(self, i):
+        self.A.ggml_m4_phase_kvwrite(self.curs[i], self.wkvas[i], self.nw, self.kcs[i], self.kidx, self.pos, self.rope,
+                                     out=self.kcur)
+
+    def wkb(self, i):
+        self.A.ggml_m4_wkb(self.wkbs[i], self.qs[i][:, :, :self.d_n], out=self.qcur[:, :, :self.d_lat])
+
+    def concat(self, i):
+        self.qcur[:, :, self.d_lat:].copy_(self.qs[i][:, :, self.d_n:])
+
+    def kqkv(self, i):
+        self.A.ggml_m4_kqkv(self.kcs[i], self.qcur, self.mask, self.kq_scale, out=self.kqv, workspace=self.ws)
+
+    def wvb(self, i):
+        self.A.ggml_m4_phase_wvb(self.wvbs[i], self.kqv, out=self.out)
+
+    def step(self, i):
+        for op in self.ops.values():
+            op(i)
+
+    def record(self, steps, warmup, reps=8):
+        us, wall, w0 = self.run_steps(steps, warmup)
+        per_op = {k: self.time_graph(self.capture(f, self.glen), reps, self.glen) for k, f in self.ops.items()}
+        total = sum(self.bytes.values())
+        return {"n_kv": self.W, "chain": " -> ".join(self.ops), "us_layer": round(us, 3), "wall_s_timed": round(wall, 6),
+                "rotating_copies": self.n_rot, "steps_per_graph": self.glen, "timed_rotation_start": w0,
+                "us_per_op_alone": {k: round(v, 3) for k, v in per_op.items()},
+                "sum_of_ops_alone": round(sum(per_op.values()), 3),
+                "alg_bytes": total, "GBps": round(total / (us * 1e3), 1),
+                "frac_of_hbm_peak": round(total / (us * 1e3) / HBM_PEAK_GBPS, 4),
+                "kqkv_splits": self.A.default_splits(self.W, self.H)}
+
+
+def layer_bench(args) -> int:
+    """--layer: us per attention layer, COLD, at both geometries and two windows (one JSON line)."""
+    import torch
+    res = {}
+    for geom, name in (("ref", "ref_kv320_q8wkb"), ("baseline", "baseline_kv576_f32wkb")):
+        res[name] = {}
+        for n_kv in (4096, 32768):
+            lay = Layer(geom, n_kv)
+            res[name][str(n_kv)] = lay.record(args.steps, args.warmup)
+            del lay
+            torch.cuda.empty_cache()
+    v = res["ref_kv320_q8wkb"]["32768"]["us_layer"]
+    rec = {"metric": "us per MLA attention layer of one decode token (COLD)", "value": v, "unit": "us/layer",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "scaling": "weak",
+           "vs_baseline": None, "dtype": "q8_0/f16/f32", "data": "synthetic",
+           "config": {"workload": "value: reference geometry (KV row 320, Q8_0 weights), 32,768-key window, "
+                                  "KV-write -> WKB -> concat -> KQKV -> wv_b in one hipGraph of whole rotations"},
+           "layers": res,
+           "reference_rx9070": {"m4_ops_in_situ": "core -18.7 us/layer for WKB (engine/m1_session.h:155-158)",
+                                "kvwrite_group_stock_us": 29.4, "wvb_stock_us": 16.6}}
+    print(json.dumps(rec), flush=True)
+    return 0
 
 
 def cpu_run(inp, threads, runs):
@@ -310,8 +465,13 @@ def decode_timings(d, steps, warmup, reps, sweep):
          "partial_kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S, d.q8),
          "partial_bytes_written": int(d.part.numel() * 4),
          "warm_us_step": round(d.warm_step(reps), 3)}
-    r["roofline"] = {"kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S, d.q8), "alg_bytes_per_launch": int(d.bytes_attn),
-                     "us_per_launch": k["partial"], "timing": "graph of back-to-back launches"}
+    if d.flat:
+        r["roofline"] = {"kernel": f"kqkv_flat_kernel<{'f16' if d.inp.kc_f16 else 'f32'} cache>",
+                         "alg_bytes_per_launch": int(d.bytes_attn), "us_per_launch": k["kqkv"],
+                         "timing": "graph of back-to-back launches", "splits": (d.W + 31) // 32}
+    else:
+        r["roofline"] = {"kernel": partial_kernel_name(d.inp.kc_f16, d.W, d.S, d.q8), "alg_bytes_per_launch": int(d.bytes_attn),
+                         "us_per_launch": k["partial"], "timing": "graph of back-to-back launches", "splits": d.S}
     if sweep:
         r["split_sweep"] = d.split_sweep(reps)
     return r
@@ -321,7 +481,7 @@ def decode_record(inp, args, steps, warmup, reps, sweep, cpu_runs, cpu_thr):
     """decode_timings of one config, the CPU oracle beside it and the error of one GPU step."""
     d = Decode(inp, args.splits)
     rec = decode_timings(d, steps, warmup, reps, sweep)
-    rec.pop("roofline")
+    rec["splits"] = rec.pop("roofline")["splits"]
     out = d.gpu_output()
     if cpu_runs:
         t, ref = cpu_run(inp, cpu_thr, cpu_runs)
@@ -348,6 +508,8 @@ def main() -> int:
     A.load_library()
     if args.ops:
         return ops_bench(args)
+    if args.layer:
+        return layer_bench(args)
     if args.batch:
         region = 32768 // args.batch
         inp = I.make_batch(args.batch, region, lens=[region] * args.batch)
@@ -372,6 +534,7 @@ def main() -> int:
     W, S, H = d.W, d.S, d.H
     us_step = t["us_step"]
     roof = t.pop("roofline")
+    S = roof.pop("splits")
     extra = {k: v for k, v in t.items() if k not in ("n_kv", "nt", "splits", "cache", "steps", "warmup")}
     del d
     torch.cuda.empty_cache()
@@ -413,7 +576,8 @@ def main() -> int:
             traffic = int(tr["traffic_bytes"])
 
     gbps = roof["alg_bytes_per_launch"] / (roof["us_per_launch"] * 1e3)
-    step_desc = "WKB + split-K partial + PHASE merge"
+    step_desc = ("WKB + one-launch KQKV (32-key splits, merged in the kernel)" if extra["kqkv_path"].startswith("one")
+                 else "WKB + split-K partial + PHASE merge")
     rec = {
         "metric": METRIC, "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1000.0, 6), "higher_is_better": False,
