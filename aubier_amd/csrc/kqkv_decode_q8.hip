@@ -12,10 +12,13 @@
 //     with its 16 mask values into its own slot of a two-stage int8 ring by LDS DMA.  The first two
 //     tiles go out right after the q block, so all of a 32K-key split is in flight from the start:
 //     unlike the f16 kernel, the q staging does not share LDS with the stream;
-//   * per tile: barrier (every wave is past the previous tile's P.V) -> each wave dequantises its
-//     slice into the f16 tile -> it issues the DMA of tile k + 2 into the slot it has just read ->
-//     the f16 kernel's Q.K^T of its own slice, scores, the maxima exchange (a barrier, after which
-//     the whole f16 tile is in place), lazy reference max and P.V;
+//   * per tile: barrier (every wave is past the previous tile's P.V) -> each wave's Q.K^T of its
+//     own slice straight from the int8 rows, each MFMA A fragment (8 values of one Q8_0 block)
+//     dequantised in registers and also stored into the wave's slot of the f16 tile -> it issues
+//     the DMA of tile k + 2 into the int8 slot it has just read -> scores, the maxima exchange (a
+//     barrier, after which the whole f16 tile is in place), lazy reference max and P.V (the f16
+//     kernel's, on the f16 tile).  The conversion's VALU work runs under the Q.K^T MFMAs of the
+//     same wave rather than in a pass of its own;
 //   * dequantisation: f16(q * d), the value a conversion of the dequantised f32 to f16 gives (the
 //     product q * d is exact in f32, so both round once): each int8 enters f16 exactly as
 //     (1024 + (q + 128)) - 1152 (the byte biased by 128 under the f16 bit pattern of 1024, then
@@ -82,51 +85,88 @@ __device__ __forceinline__ void q8_dma(const SliceStream<DK> & ss, uint32_t ring
     dma4(mrs, 4u * (uint32_t)(lane & 15), 0u, sb + (uint32_t)G8::ROWS_BYTES);
 }
 
-// Wave w's int8 slice at src -> f16 values in its slot of the tile at dst (the slot layout of
-// decode_common.h, slot_byte).  Lane item i: row r = lane & 15, half-block hb = (lane >> 4) + 4 i (16
-// values of block b = hb / 2, at bytes 34 b + 2 + 16 (hb & 1) of the row: 2-byte aligned, read as
-// five dwords and realigned).  The 16 lanes of a group read 16 rows, 612 bytes (153 dwords) apart:
-// distinct LDS banks.  Items go in batches of IB whose reads all issue before the first convert.
-template <int DK>
-__device__ __forceinline__ void dequant_slice(const char * src, char * dst, int lane) {
-    using G8 = Q8Geom<DK>;
-    static_assert(G8::HB % 4 == 0 && G8::ITEMS * 4 == G8::HB, "four half-block groups per row");
-    constexpr int IB = G8::ITEMS % 3 == 0 ? 3 : 1;
-    const half2 bias = {1152.0f16, 1152.0f16};            // 1024 + 128
-    const int r = lane & 15;
-    const char * row = src + r * G8::ROWB;
-#pragma unroll
-    for (int i0 = 0; i0 < G8::ITEMS; i0 += IB) {
-        uint32_t wd[IB][5];
-        half_t d[IB];
-        int hb[IB];
-#pragma unroll
-        for (int u = 0; u < IB; ++u) {
-            hb[u] = (lane >> 4) + 4 * (i0 + u);
-            const int o = 34 * (hb[u] >> 1) + 2 + 16 * (hb[u] & 1);
-            const uint32_t * p = reinterpret_cast<const uint32_t *>(row + (o & ~3));
-#pragma unroll
-            for (int k = 0; k < 5; ++k) wd[u][k] = p[k];
-            d[u] = *reinterpret_cast<const half_t *>(row + 34 * (hb[u] >> 1));
-        }
-#pragma unroll
-        for (int u = 0; u < IB; ++u) {
-            const uint32_t sh = (hb[u] & 2) ? 0u : 2u;       // 34 b + 2 + 16 h = 2 (b + 1) mod 4
-            const half2 dd = {d[u], d[u]};
-            uint32_t ow[8];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t x = __builtin_amdgcn_alignbyte(wd[u][k + 1], wd[u][k], sh) ^ 0x80808080u;   // q + 128 per byte
-                const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);   // bytes 0, 1 under 0x64
-                const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);   // bytes 2, 3 under 0x64
-                ow[2 * k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2, lo) - bias) * dd);
-                ow[2 * k + 1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2, hi) - bias) * dd);
-            }
-            const int c0 = 2 * hb[u];                         // 16-byte chunks c0, c0 + 1 of row r
-            *reinterpret_cast<u32x4 *>(dst + slot_byte(r, c0)) = u32x4{ow[0], ow[1], ow[2], ow[3]};
-            *reinterpret_cast<u32x4 *>(dst + slot_byte(r, c0 + 1)) = u32x4{ow[4], ow[5], ow[6], ow[7]};
-        }
+// Eight int8 values and their block scale d -> f16(q * d).  w0..w2: the aligned dwords that hold
+// the values from byte SH of w0 on (SH = 0: w0, w1 alone).  Each byte enters f16 exactly as
+// (1024 + (q + 128)) - 1152 (the byte biased by 128 under the f16 bit pattern of 1024), then one
+// multiplication by d rounds once: the value a conversion of the exact f32 product q * d gives.
+template <int SH>
+__device__ __forceinline__ half8 q8x8_to_f16(uint32_t w0, uint32_t w1, uint32_t w2, half_t d) {
+    const half2 bias = {1152.0f16, 1152.0f16};
+    const half2 dd = {d, d};
+    uint32_t x[2];
+    if constexpr (SH == 0) {
+        x[0] = w0;
+        x[1] = w1;
+    } else {
+        x[0] = __builtin_amdgcn_alignbyte(w1, w0, SH);
+        x[1] = __builtin_amdgcn_alignbyte(w2, w1, SH);
     }
+    half8 r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t y = x[k] ^ 0x80808080u;                                   // q + 128 per byte
+        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, y, 0x04010400u);  // bytes 0, 1 under 0x64
+        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, y, 0x04030402u);  // bytes 2, 3 under 0x64
+        const half2 a = (__builtin_bit_cast(half2, lo) - bias) * dd;
+        const half2 b = (__builtin_bit_cast(half2, hi) - bias) * dd;
+        r[4 * k] = a[0];
+        r[4 * k + 1] = a[1];
+        r[4 * k + 2] = b[0];
+        r[4 * k + 3] = b[1];
+    }
+    return r;
+}
+
+// S^T = K . Q^T for the wave's 16 keys, straight from its int8 slice at src (C rows = keys 4 g + r,
+// C cols = heads j16 (s0) and 16 + j16 (s1)), dequantising each A fragment in registers: step s is
+// Q8_0 block s of every row (D_k / 32 blocks = the K-steps of the 16x16x32 MFMA), lane (j16, g)
+// taking values 8 g .. 8 g + 7 of block s of row j16 -- 8 bytes at 34 s + 2 + 8 g of the row, 4-byte
+// aligned for odd s, 2 bytes past it for even s (rows are 612 bytes, a multiple of 4) -- and the
+// block's scale.  Each converted fragment is also stored to its place in the f16 slot at dst (the
+// layout of decode_common.h, slot_byte: chunk 4 s + g of row j16) when P.V reads it (the first D_v
+// values of a row: steps s < D_v / 32), after the maxima barrier, so the dequantisation's VALU work
+// runs under the Q.K^T MFMAs instead of in a pass of its own.  Operand reads run PF steps ahead of
+// their conversion.  Every DMA of the slice has landed.
+template <int DK, int DV>
+__device__ __forceinline__ void qk_slice_q8(const char * src, char * dst, int lane,
+                                            const half8 (&qreg)[2][SliceGeom<DK>::QSTEPS], f32x4 & s0, f32x4 & s1) {
+    using G = SliceGeom<DK>;
+    using G8 = Q8Geom<DK>;
+    static_assert(G::QSTEPS == DK / 32 && G8::ROWB % 4 == 0, "one Q8_0 block per K-step, dword-aligned rows");
+    constexpr int PF = 4;
+    const int g = lane >> 4, j16 = lane & 15;
+    const char * row = src + j16 * G8::ROWB;
+    const int a0 = slot_byte(j16, g);
+    uint32_t raw[PF][3];
+    half_t dsc[PF];
+    auto rd = [&](int s) {
+        const int b = 34 * s + 2 + 8 * g;                  // = 2 (mod 4) for even s, 0 for odd s
+        const uint32_t * p = reinterpret_cast<const uint32_t *>(row + (b & ~3));
+        raw[s % PF][0] = p[0];
+        raw[s % PF][1] = p[1];
+        if ((s & 1) == 0) raw[s % PF][2] = p[2];
+        dsc[s % PF] = *reinterpret_cast<const half_t *>(row + 34 * s);
+    };
+#pragma unroll
+    for (int s = 0; s < PF; ++s) rd(s);
+    f32x4 acc0, acc1, acc2, acc3;
+#pragma unroll
+    for (int s = 0; s < G::QSTEPS; ++s) {
+        const uint32_t * r = raw[s % PF];
+        const half8 av = (s & 1) ? q8x8_to_f16<0>(r[0], r[1], 0u, dsc[s % PF]) : q8x8_to_f16<2>(r[0], r[1], r[2], dsc[s % PF]);
+        if (s + PF < G::QSTEPS) rd(s + PF);
+        if (32 * s < DV) *reinterpret_cast<half8 *>(dst + (a0 ^ (64 * (s & 1))) + 2048 * (s >> 1)) = av;
+        if (s & 1) {
+            mfma16<false>(acc2, av, qreg[0][s], s == 1);
+            mfma16<false>(acc3, av, qreg[1][s], s == 1);
+        } else {
+            mfma16<false>(acc0, av, qreg[0][s], s == 0);
+            mfma16<false>(acc1, av, qreg[1][s], s == 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    s0 = acc0 + acc2;
+    s1 = acc1 + acc3;
 }
 
 // One row (token) t of the split: the whole pass, from the q staging to the partial record.
@@ -180,18 +220,19 @@ __device__ __forceinline__ void decode_row_q8(const DecodeArgs & a, int t, Q8Lds
         else wait_vm<0>();
         if (k > 0) __syncthreads();          // every wave is past the P.V of tile k - 1
         const char * src = sh.ring8 + (s * NWAVE + w) * G8::SLOT;
-        dequant_slice<DK>(src, sb, lane);
+        // Q.K^T from the int8 slice, which also writes the slice's f16 values for P.V (which reads
+        // every slice, after the maxima barrier below)
+        f32x4 s0, s1;
+        qk_slice_q8<DK, DV>(src, sb, lane, qreg, s0, s1);
         const f32x4 mk = *reinterpret_cast<const f32x4 *>(src + G8::ROWS_BYTES + 16 * g);
-        if (k + 2 < n_my) {                  // the slot has been read: tile k + 2 takes it
+        // the slot has been read: tile k + 2 takes it.  One burst here measured faster than the same
+        // instructions spread over the P.V MFMAs (2.60 against 2.85 us per tile at 16 tiles a split):
+        // the address unit's time (16 B a lane) stalls the issuing wave either way, and between MFMAs
+        // it holds them back as well
+        if (k + 2 < n_my) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             q8_dma<DK>(ss, ring8, s, k + 2, lane);
         }
-        // no barrier here: Q.K^T reads only this wave's own slice (its LDS accesses are in order),
-        // and P.V, which reads every slice, follows the maxima barrier below, which every wave
-        // reaches after its dequantisation
-
-        f32x4 s0, s1;
-        qk_slice<DK, false, false>(ss, SliceDma{}, sb, lane, qreg, s0, s1);
         const int par = k & 1;
         const int kbase = (ss.t0 + k) * TK + WK * w;
         float sc[2][4], mx[2];
@@ -303,22 +344,20 @@ __global__ __launch_bounds__(256) void q8_rows_to_f16_kernel(const char * __rest
     const int o = 34 * (hb >> 1) + 2 + 16 * (hb & 1);
     const uint32_t sh = (hb & 2) ? 0u : 2u;                          // 34 b + 2 + 16 h = 2 (b + 1) mod 4
     const uint32_t * p = reinterpret_cast<const uint32_t *>(r + (o & ~3));
-    const uint32_t wd[5] = {p[0], p[1], p[2], p[3], sh ? p[4] : 0u};
     const half_t d = *reinterpret_cast<const half_t *>(r + 34 * (hb >> 1));
-    const half2 bias = {1152.0f16, 1152.0f16};
-    const half2 dd = {d, d};
-    uint32_t ow[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t x = __builtin_amdgcn_alignbyte(wd[k + 1], wd[k], sh) ^ 0x80808080u;
-        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
-        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
-        ow[2 * k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2, lo) - bias) * dd);
-        ow[2 * k + 1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2, hi) - bias) * dd);
+    half8 v0, v1;
+    if (sh) {
+        const uint32_t wd[5] = {p[0], p[1], p[2], p[3], p[4]};
+        v0 = q8x8_to_f16<2>(wd[0], wd[1], wd[2], d);
+        v1 = q8x8_to_f16<2>(wd[2], wd[3], wd[4], d);
+    } else {
+        const uint32_t wd[4] = {p[0], p[1], p[2], p[3]};
+        v0 = q8x8_to_f16<0>(wd[0], wd[1], 0u, d);
+        v1 = q8x8_to_f16<0>(wd[2], wd[3], 0u, d);
     }
-    u32x4 * out = reinterpret_cast<u32x4 *>(dst + row * DK + 16 * hb);
-    out[0] = u32x4{ow[0], ow[1], ow[2], ow[3]};
-    out[1] = u32x4{ow[4], ow[5], ow[6], ow[7]};
+    half8 * out = reinterpret_cast<half8 *>(dst + row * DK + 16 * hb);
+    out[0] = v0;
+    out[1] = v1;
 }
 
 template <int DK, int DV>

@@ -24,6 +24,8 @@ BUDGET = {
     "kqkv_decode_q8_kernel": (0, 0),
     "kqkv_prefill_f16_kernel": (24, 128),
     "kqkv_generic_kernel": (0, 0),
+    "kqkv_flat_kernel": (0, 0),
+    "q8_rows_to_f16_kernel": (0, 0),
     "merge_kernel": (0, 0),
     "merge_few_kernel": (0, 0),
     "wkb_f32_kernel": (0, 0),
