@@ -251,6 +251,8 @@ int check_wkb(const mla_m4_tensor * w, const mla_m4_tensor * x, const mla_m4_ten
     if (dst->nb[1] < (size_t)dv * 4) return MLA_M4_ERR_STRIDE;
     if (dn != 64 && dn != 128) return MLA_M4_ERR_UNSUPPORTED;
     if (dv % 16 != 0 || nh * dv > INT32_MAX || x->ne[2] > INT32_MAX) return MLA_M4_ERR_UNSUPPORTED;
+    // the GEMM path (16 tokens and more) addresses 8 token rows of q from one buffer base
+    if (x->ne[2] >= 16 && x->nb[2] > UINT32_MAX / 8) return MLA_M4_ERR_UNSUPPORTED;
     return MLA_M4_OK;
 }
 

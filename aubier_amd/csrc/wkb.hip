@@ -73,35 +73,74 @@ __global__ __launch_bounds__(256) void wkb_f32_kernel(WkbArgs a) {
 }
 
 // Many tokens (chunked prefill): per head a GEMM dst_h[t][c] = sum_d q_h[t][d] W_h[c][d], on
-// v_mfma_f32_32x32x2_f32 (f32 products and sums, as the f32 mul_mat).  A workgroup computes 128
-// tokens x 128 columns of one head, each wave a 64 x 64 quarter (2 x 2 tiles of 32 x 32).  Both
-// operands have d contiguous, so a lane reads 4 consecutive d of its row (16 bytes) and spends them
-// on 4 MFMA k-steps: step j uses d = 8 p + 4 (lane >> 5) + j in A and B alike (the k order inside
-// an MFMA is free as long as both operands agree).  Operands come straight from global memory
-// (L2-resident: each q tile is read by D_v/128 workgroups, each W tile by nt/128) one 8-d block
-// ahead of their MFMAs.
+// v_mfma_f32_32x32x2_f32 (f32 products and sums, as the f32 mul_mat).  A workgroup computes a
+// 128-token x 128-column tile of one head, each wave a 64 x 64 quarter (2 x 2 tiles of 32 x 32).
+// The operands pass through LDS in d-chunks of 32 (128 bytes of every row): the chunk's q rows (A)
+// and W rows (B) arrive by LDS DMA, 8 lanes fetching one row's whole 128-byte line, in a two-stage
+// ring (64 KB), the next chunk's DMA in flight while the MFMAs run on this one.  Row r of a stage
+// keeps its 8 16-byte chunks at slot c ^ (r & 7), so the fragment reads (32 rows at one chunk)
+// cover every bank once per 8 lanes.  A lane reads 4 consecutive d of its row (16 bytes) and
+// spends them on 4 MFMA k-steps: step j uses d = 8 p + 4 (lane >> 5) + j in A and B alike (the k
+// order inside an MFMA is free as long as both operands agree).  Tiles are ordered so that the
+// tiles of a head run on one XCD (workgroup i is dispatched to XCD i mod 8), which keeps each
+// head's q and W rows in one L2.
 constexpr int WKB_GEMM_MIN_TOKENS = 16;
+constexpr int WG_T = 128;                   // tile rows (tokens) and columns
+constexpr int WG_DC = 32;                   // d per chunk
+constexpr int WG_STAGE = WG_T * WG_DC * 4;  // bytes of one operand in one stage (16 KB)
+
+struct WkbGemmLds {
+    __attribute__((aligned(16))) char a[2][WG_STAGE];
+    __attribute__((aligned(16))) char b[2][WG_STAGE];
+};
 
 __global__ __launch_bounds__(256) void wkb_gemm_kernel(WkbArgs a) {
+    __shared__ WkbGemmLds sh;
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int h = blockIdx.z;
-    const int tw = blockIdx.y * 128 + 64 * (w >> 1);     // this wave's first token
-    const int cw = blockIdx.x * 128 + 64 * (w & 1);      // and first column
-    const int r32 = lane & 31, hh = lane >> 5;
-    const char * qb = reinterpret_cast<const char *>(a.q) + (size_t)h * a.q_nb1;
-    const float * wb = a.w + (size_t)h * a.d_v * a.d_n;
-    const float * arow[2];
-    const float * brow[2];
-    bool av[2];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ntb = (a.nt + WG_T - 1) / WG_T, ncb = (a.d_v + WG_T - 1) / WG_T;
+    const int per_head = ntb * ncb;
+    const int total = a.n_head * per_head;
+    int lt = blockIdx.x;
+    if ((total & 7) == 0) lt = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int h = lt / per_head;
+    const int tb = (lt - h * per_head) / ncb;
+    const int cb = lt - h * per_head - tb * ncb;
+    const int t0 = tb * WG_T, c0 = cb * WG_T;
+
+    // DMA plan: wave w fetches rows 8 i .. 8 i + 7 (i = 4 w .. 4 w + 3) of both operands; lane l
+    // takes row 8 i + (l >> 3), logical chunk (l & 7) ^ (row & 7), into slot l of the 1 KB block i.
+    // Each instruction's resource starts at its first row, so the lane offsets stay below 8 rows.
+    const int lr = lane >> 3;
+    const uint32_t lchunk = 16u * (uint32_t)((lane & 7) ^ lr);      // row & 7 == lr
+    const char * qh = reinterpret_cast<const char *>(a.q) + (size_t)h * a.q_nb1;
+    const char * wh = reinterpret_cast<const char *>(a.w) + (size_t)h * a.d_v * a.d_n * 4;
+    const int rowb = a.d_n * 4;
+    i32x4 ars[4], brs[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int t = tw + 32 * i + r32;
-        av[i] = t < a.nt;
-        arow[i] = reinterpret_cast<const float *>(qb + (size_t)min(t, a.nt - 1) * a.q_nb2) + 4 * hh;
-        const int c = min(cw + 32 * i + r32, a.d_v - 1);
-        brow[i] = wb + (size_t)c * a.d_n + 4 * hh;
+    for (int u = 0; u < 4; ++u) {
+        const int r0 = 8 * (4 * w + u);
+        const int ra = min(a.nt - t0 - r0, 8), rb = min(a.d_v - c0 - r0, 8);     // rows that exist
+        ars[u] = make_rsrc(qh + (size_t)(t0 + r0) * a.q_nb2, ra > 0 ? (uint32_t)((int64_t)(ra - 1) * a.q_nb2 + rowb) : 0u);
+        brs[u] = make_rsrc(wh + (size_t)(c0 + r0) * rowb, rb > 0 ? (uint32_t)(rb * rowb) : 0u);
     }
+    const uint32_t avo = (uint32_t)(lr * a.q_nb2) + lchunk, bvo = (uint32_t)(lr * rowb) + lchunk;
+    auto dma_chunk = [&](int kc, int st) {
+        const uint32_t la = lds_addr(sh.a[st]), lb = lds_addr(sh.b[st]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t blk = 1024u * (uint32_t)(4 * w + u);
+            dma16(ars[u], avo + (uint32_t)(WG_DC * 4 * kc), 0u, la + blk);
+            dma16(brs[u], bvo + (uint32_t)(WG_DC * 4 * kc), 0u, lb + blk);
+        }
+    };
+
+    // fragment addresses: A rows 64 (w >> 1) + 32 i + (lane & 31), B rows 64 (w & 1) + 32 j + (lane & 31)
+    const int r32 = lane & 31, hh = lane >> 5;
+    const int sw = r32 & 7;
+    const int apitch = WG_DC * 4;            // a stage row: 128 bytes
+    const int aoff = apitch * (64 * (w >> 1) + r32), boff = apitch * (64 * (w & 1) + r32);
+
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -109,33 +148,42 @@ __global__ __launch_bounds__(256) void wkb_gemm_kernel(WkbArgs a) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    const int np = a.d_n / 8;
-    f32x4 an[2], bn[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        an[i] = av[i] ? *reinterpret_cast<const f32x4 *>(arow[i]) : f32x4{0.f, 0.f, 0.f, 0.f};
-        bn[i] = *reinterpret_cast<const f32x4 *>(brow[i]);
-    }
-    for (int p = 0; p < np; ++p) {
-        const f32x4 ac[2] = {an[0], an[1]};
-        const f32x4 bc[2] = {bn[0], bn[1]};
-        if (p + 1 < np) {
+
+    const int nch = a.d_n / WG_DC;
+    dma_chunk(0, 0);
+    for (int kc = 0; kc < nch; ++kc) {
+        const int st = kc & 1;
+        wait_vm<0>();                        // this wave's part of chunk kc has landed
+        __syncthreads();                     // every wave's part; every wave is past chunk kc - 1
+        if (kc + 1 < nch) dma_chunk(kc + 1, st ^ 1);
+        const char * sa = sh.a[st];
+        const char * sb = sh.b[st];
+        f32x4 af[2][2], bf[2][2];
+        auto load = [&](int p, int buf) {
+            const int slot = 16 * ((2 * p + hh) ^ sw);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                an[i] = av[i] ? *reinterpret_cast<const f32x4 *>(arow[i] + 8 * (p + 1)) : f32x4{0.f, 0.f, 0.f, 0.f};
-                bn[i] = *reinterpret_cast<const f32x4 *>(brow[i] + 8 * (p + 1));
+                af[buf][i] = *reinterpret_cast<const f32x4 *>(sa + aoff + apitch * 32 * i + slot);
+                bf[buf][i] = *reinterpret_cast<const f32x4 *>(sb + boff + apitch * 32 * i + slot);
             }
+        };
+        load(0, 0);
+#pragma unroll
+        for (int p = 0; p < WG_DC / 8; ++p) {
+            if (p + 1 < WG_DC / 8) load(p + 1, (p + 1) & 1);
+#pragma unroll
+            for (int j4 = 0; j4 < 4; ++j4)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[p & 1][i][j4], bf[p & 1][j][j4], acc[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int j4 = 0; j4 < 4; ++j4)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ac[i][j4], bc[j][j4], acc[i][j], 0, 0, 0);
     }
-    // C tile (i, j): lane column c = cw + 32 j + (lane & 31), rows t = tw + 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3)
+    // C tile (i, j): lane column c = c0 + 64 (w & 1) + 32 j + (lane & 31), rows
+    // t = t0 + 64 (w >> 1) + 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3)
     char * db = reinterpret_cast<char *>(a.dst) + (size_t)h * a.d_nb1;
+    const int tw = t0 + 64 * (w >> 1), cw = c0 + 64 * (w & 1);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -153,9 +201,12 @@ __global__ __launch_bounds__(256) void wkb_gemm_kernel(WkbArgs a) {
 }  // namespace
 
 hipError_t launch_wkb_f32(const WkbArgs & a, hipStream_t stream) {
-    if (a.nt >= WKB_GEMM_MIN_TOKENS && a.d_n % 8 == 0) {
-        const dim3 grid((a.d_v + 127) / 128, (a.nt + 127) / 128, a.n_head);
-        hipLaunchKernelGGL(wkb_gemm_kernel, grid, dim3(256), 0, stream, a);
+    if (a.nt >= WKB_GEMM_MIN_TOKENS && a.d_n % WG_DC == 0) {
+        // one 8-row DMA window of q must stay within the buffer's 32-bit offsets
+        if (a.q_nb2 > (int64_t)(UINT32_MAX / 8)) return hipErrorInvalidValue;
+        const int64_t tiles = (int64_t)a.n_head * ((a.nt + WG_T - 1) / WG_T) * ((a.d_v + WG_T - 1) / WG_T);
+        if (tiles > INT32_MAX) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(wkb_gemm_kernel, dim3((unsigned)tiles), dim3(256), 0, stream, a);
         return hipGetLastError();
     }
     const int total = a.n_head * a.d_v;
