@@ -7,7 +7,7 @@
 // owns 8 (d_n = 128) or 16 (d_n = 64) consecutive rows of one head, issues all its 16-byte row
 // loads before the first use, and reduces each row over its d_n/4 lanes with xor shuffles.  For
 // a few tokens the rows stay in registers while the tokens stream past; from 16 tokens on the op
-// is a batched GEMM and runs on f32 MFMA (wkb_gemm_kernel).
+// is a batched GEMM and runs on MFMA (wkb_gemm_kernel, f32 operands split into f16 pieces).
 #include "mla_common.h"
 #include "mla_kernels.h"
 
@@ -72,18 +72,26 @@ __global__ __launch_bounds__(256) void wkb_f32_kernel(WkbArgs a) {
     }
 }
 
-// Many tokens (chunked prefill): per head a GEMM dst_h[t][c] = sum_d q_h[t][d] W_h[c][d], on
-// v_mfma_f32_32x32x2_f32 (f32 products and sums, as the f32 mul_mat).  A workgroup computes a
-// 128-token x 128-column tile of one head, each wave a 64 x 64 quarter (2 x 2 tiles of 32 x 32).
-// The operands pass through LDS in d-chunks of 32 (128 bytes of every row): the chunk's q rows (A)
-// and W rows (B) arrive by LDS DMA, 8 lanes fetching one row's whole 128-byte line, in a two-stage
-// ring (64 KB), the next chunk's DMA in flight while the MFMAs run on this one.  Row r of a stage
-// keeps its 8 16-byte chunks at slot c ^ (r & 7), so the fragment reads (32 rows at one chunk)
-// cover every bank once per 8 lanes.  A lane reads 4 consecutive d of its row (16 bytes) and
-// spends them on 4 MFMA k-steps: step j uses d = 8 p + 4 (lane >> 5) + j in A and B alike (the k
-// order inside an MFMA is free as long as both operands agree).  Tiles are ordered so that the
-// tiles of a head run on one XCD (workgroup i is dispatched to XCD i mod 8), which keeps each
-// head's q and W rows in one L2.
+// Many tokens (chunked prefill): per head a GEMM dst_h[t][c] = sum_d q_h[t][d] W_h[c][d] with f32
+// operands, run on the 16-bit MFMA: each operand value x is split into two f16 pieces,
+// hi = f16(x) and lo = f16(2^11 (x - hi)) (x - hi is exact in f32), which carry 22 bits of x, and
+// x.y = hi.hi + 2^-11 (hi.lo + lo.hi) up to lo.lo (below 2^-22 of the product).  Three
+// v_mfma_f32_32x32x16_f16 per 16-d step, f32 accumulation (hi.hi on one accumulator, the cross
+// terms on a second, added at the end): 5.3x the operand throughput of v_mfma_f32_32x32x2_f32 for
+// results within a few f32 ulps of the f32 product.  A 16-d step of a wave whose largest operand
+// magnitude is 2^15 or more (hi would overflow f16) or below 2^-8 (its values would sit in f16's
+// subnormal range) runs on v_mfma_f32_32x32x2_f32 instead, on the same accumulator.
+// A workgroup computes a 128-token x 128-column tile of one head, each wave a 64 x 64 quarter
+// (2 x 2 tiles of 32 x 32).  The operands pass through LDS in d-chunks of 32 (128 bytes of every
+// row): the chunk's q rows (A) and W rows (B) arrive by LDS DMA, 8 lanes fetching one row's whole
+// 128-byte line, in a two-stage ring (64 KB), the next chunk's DMA in flight while the MFMAs run on
+// this one.  Row r of a stage keeps its 8 16-byte chunks at slot c ^ (r & 7), so the fragment reads
+// (32 rows at one chunk) cover every bank once per 8 lanes.  A lane reads 8 consecutive d of its
+// row per 16-d step, the k index of the f16 MFMA (or, on the f32 path, d = 16 ks + 8 (lane >> 5) + e
+// is k-step e, in A and B alike: the k order inside an MFMA is free as long as both operands
+// agree).  Tiles are ordered so that the tiles of a head run on one XCD (workgroup i is dispatched
+// to XCD i mod 8), which keeps each head's q and W rows in one L2.  Two workgroups share a CU
+// (LDS-bound), so the kernel is held to 256 registers per lane.
 constexpr int WKB_GEMM_MIN_TOKENS = 16;
 constexpr int WG_T = 128;                   // tile rows (tokens) and columns
 constexpr int WG_DC = 32;                   // d per chunk
@@ -94,7 +102,7 @@ struct WkbGemmLds {
     __attribute__((aligned(16))) char b[2][WG_STAGE];
 };
 
-__global__ __launch_bounds__(256) void wkb_gemm_kernel(WkbArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wkb_gemm_kernel(WkbArgs a) {
     __shared__ WkbGemmLds sh;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -141,13 +149,17 @@ __global__ __launch_bounds__(256) void wkb_gemm_kernel(WkbArgs a) {
     const int apitch = WG_DC * 4;            // a stage row: 128 bytes
     const int aoff = apitch * (64 * (w >> 1) + r32), boff = apitch * (64 * (w & 1) + r32);
 
-    f32x16 acc[2][2];
+    // acc: the f32 sum; accx: the cross terms of the f16 split, in units of 2^-11
+    f32x16 acc[2][2], accx[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < 16; ++r) {
+                acc[i][j][r] = 0.0f;
+                accx[i][j][r] = 0.0f;
+            }
 
     const int nch = a.d_n / WG_DC;
     dma_chunk(0, 0);
@@ -158,28 +170,74 @@ __global__ __launch_bounds__(256) void wkb_gemm_kernel(WkbArgs a) {
         if (kc + 1 < nch) dma_chunk(kc + 1, st ^ 1);
         const char * sa = sh.a[st];
         const char * sb = sh.b[st];
-        f32x4 af[2][2], bf[2][2];
-        auto load = [&](int p, int buf) {
-            const int slot = 16 * ((2 * p + hh) ^ sw);
+        // per 16-d k-step ks: the wave's operands, row 32 i + (lane & 31) of its A / B rows,
+        // d = 16 ks + 8 hh .. + 7 (logical 16-byte chunks 4 ks + 2 hh, + 1)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                af[buf][i] = *reinterpret_cast<const f32x4 *>(sa + aoff + apitch * 32 * i + slot);
-                bf[buf][i] = *reinterpret_cast<const f32x4 *>(sb + boff + apitch * 32 * i + slot);
-            }
-        };
-        load(0, 0);
+        for (int ks = 0; ks < 2; ++ks) {
+            f32x4 af[2][2], bf[2][2];            // [tile][half]
 #pragma unroll
-        for (int p = 0; p < WG_DC / 8; ++p) {
-            if (p + 1 < WG_DC / 8) load(p + 1, (p + 1) & 1);
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j4 = 0; j4 < 4; ++j4)
+                for (int u = 0; u < 2; ++u) {
+                    const int slot = 16 * ((4 * ks + 2 * hh + u) ^ sw);
+                    af[i][u] = *reinterpret_cast<const f32x4 *>(sa + aoff + apitch * 32 * i + slot);
+                    bf[i][u] = *reinterpret_cast<const f32x4 *>(sb + boff + apitch * 32 * i + slot);
+                }
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fmaxf(fabsf(af[i][u][e]), fabsf(bf[i][u][e])));
+            mx = wave_max(mx);
+            if (mx < 32768.0f && (mx >= 0.00390625f || mx == 0.0f)) {
+                // x = hi + 2^-11 lo with hi = f16(x), lo = f16(2^11 (x - hi)) (x - hi exact in f32):
+                // 22 bits of x.  hi.hi on one accumulator, hi.lo + lo.hi on the other (lo.lo, below
+                // 2^-22 of the product, is dropped)
+                auto split = [](const f32x4 & x0, const f32x4 & x1, half8 & hi, half8 & lo) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float x = e < 4 ? x0[e] : x1[e - 4];
+                        const half_t h = (half_t)x;
+                        hi[e] = h;
+                        lo[e] = (half_t)((x - (float)h) * 2048.0f);
+                    }
+                };
+                half8 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    split(af[i][0], af[i][1], ah[i], al[i]);
+                    split(bf[i][0], bf[i][1], bh[i], bl[i]);
+                }
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[p & 1][i][j4], bf[p & 1][j][j4], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < 2; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                        accx[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], accx[i][j], 0, 0, 0);
+                        accx[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], accx[i][j], 0, 0, 0);
+                    }
+            } else {
+                // values the f16 pieces cannot carry (|x| >= 2^15) or a step of tiny values: f32
+                // MFMA, its k-step e taking d = 16 ks + 8 hh + e in A and B alike
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][e >> 2][e & 3], bf[j][e >> 2][e & 3],
+                                                                            acc[i][j], 0, 0, 0);
+            }
         }
     }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(accx[i][j][r], 1.0f / 2048.0f, acc[i][j][r]);
     // C tile (i, j): lane column c = c0 + 64 (w & 1) + 32 j + (lane & 31), rows
     // t = t0 + 64 (w >> 1) + 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3)
     char * db = reinterpret_cast<char *>(a.dst) + (size_t)h * a.d_nb1;

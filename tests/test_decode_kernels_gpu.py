@@ -195,6 +195,39 @@ def test_fully_masked_splits(dev, dk, dv, n_kv, nt, S):
     check(f"fully masked splits {dk}/{dv} nt={nt} S={S} vs oracle", out.cpu().numpy(), ref, 1e-2, 3e-3)
 
 
+@pytest.mark.parametrize("case", ["large_rows", "tiny", "mixed_magnitudes", "huge_weight_column"])
+def test_wkb_gemm_operand_range(dev, case):
+    """The many-token WKB GEMM splits its f32 operands into two f16 pieces (22 bits) and takes the
+    f32 MFMA for a wave's 16-d step whose largest operand is >= 2^15 or < 2^-8.  Inputs that hit
+    both paths in one launch: q rows of the first 64 tokens scaled to ~1e5 (their waves' steps on
+    f32, the other waves' on f16 pieces); everything below 2^-8 (f32 throughout); half the q values
+    scaled by 1e-6 (f16 subnormals inside an f16-piece step); one W_kb column of 4e4 (the steps that
+    hold it on f32).  Against the oracle at the f32 bar (relative to max|ref|) and against float64."""
+    H, d_v, d_n, nt = 4, 512, 128, 130
+    g = np.random.default_rng(8811 + ["large_rows", "tiny", "mixed_magnitudes", "huge_weight_column"].index(case))
+    w = g.standard_normal((H, d_v, d_n)) * 0.05
+    q = g.standard_normal((nt, H, d_n)) * 0.05
+    if case == "large_rows":
+        q[:64] *= 2e6
+    elif case == "tiny":
+        q *= 1e-3
+        w *= 1e-3
+    elif case == "mixed_magnitudes":
+        q[g.random(q.shape) < 0.5] *= 1e-6
+    else:
+        w[:, :, 5] = 4e4
+    w = w.astype(np.float32)
+    q = q.astype(np.float32)
+    ref = orc.wkb(w, q)
+    ref64 = np.einsum("hcd,thd->thc", w.astype(np.float64), q.astype(np.float64))
+    out = A.ggml_m4_wkb(torch.from_numpy(w).to(dev), torch.from_numpy(q).to(dev))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    m = float(np.abs(ref64).max())
+    check(f"WKB GEMM {case} vs oracle", got, ref, 1e-5 * m, 1e-5)
+    check(f"WKB GEMM {case} vs f64", got, ref64, 2e-6 * m, 2e-6)
+
+
 @pytest.mark.parametrize("d_n,d_v", [(128, 512), (64, 256)])
 @pytest.mark.parametrize("nt", [1, 5, 16, 37, 130])
 def test_wkb_token_counts(dev, d_n, d_v, nt):
