@@ -191,7 +191,9 @@ int mla_m4_kqkv_default_splits(int64_t n_kv, int64_t n_head, int32_t kcache_type
  *   part F32 ne [MLA_M4_PART_FLOATS(D_v) (F16 cache) or MLA_M4_PART_FLOATS_F32(D_v) (F32 cache),
  *                n_split, nt, ceil(H / 32)] contiguous (layout above);
  *   D_v is the V width the partials are for (512 for the 576-wide cache, 256 for the 320-wide).
- * Followed by mla_m4_phase_merge this equals mla_m4_kqkv.
+ * Followed by mla_m4_phase_merge this is mla_m4_kqkv's split-K path: bit for bit where mla_m4_kqkv
+ * takes that path with the same split count (F16 and F32 caches below 16 tokens, except a short
+ * window's one-launch kernel, which agrees within the cache type's bar).
  * ------------------------------------------------------------------------------------------- */
 int mla_m4_kqkv_partial(const mla_m4_tensor * kcache, const mla_m4_tensor * q,
                         const mla_m4_tensor * mask, float kq_scale, int n_split, int64_t d_v,

@@ -86,6 +86,20 @@ def test_cfg4_max_context(dev):
     assert er_k64 < er_o64 / 10              # the kernel is the closer of the two to exact
 
 
+@pytest.mark.parametrize("cfg,n_kv,nt", [(2, 4096, 1), (3, 32768, 1), (3, 32768, 3), (1, 1000, 1)])
+def test_partial_then_merge_is_kqkv_split_path(dev, cfg, n_kv, nt):
+    """mla_m4_kqkv_partial at the library's split count followed by mla_m4_phase_merge is
+    mla_m4_kqkv's split-K path bit for bit: the f16 cache's MFMA decode kernel (one token, and three
+    rows sharing a split's workgroup) and an f32 cache past the one-launch window (the VALU kernel)."""
+    inp = I.make_config(cfg, n_kv=n_kv, nt=nt)
+    g = upload(inp, dev)
+    _, out = run_step(g, inp.kq_scale)
+    S = A.default_splits(inp.n_kv, I.N_HEAD, A.ops.TYPE_F16 if inp.kc_f16 else A.ops.TYPE_F32)
+    _, out2 = run_step(g, inp.kq_scale, n_split=S)
+    say(f"cfg{cfg} n_kv={n_kv} nt={nt} S={S}: {int(np.sum(out.view(np.uint32) != out2.view(np.uint32)))} differing words")
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+
+
 def test_partials_match_oracle(dev):
     inp = I.make_config(2, n_kv=1000)
     g = upload(inp, dev)
