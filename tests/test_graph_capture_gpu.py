@@ -158,3 +158,71 @@ def test_layer_step_capture_and_replay(dev):
         # wv_b: bit-identical to the oracle's wv_b of the GPU's KQKV output
         wvb_ref = orc.wvb_q8(w_vb, D_LAT, D_OUT, H, np.ascontiguousarray(got["kqv"].transpose(1, 0, 2))).transpose(1, 0, 2)
         assert np.array_equal(got["out"].view(np.uint32), np.ascontiguousarray(wvb_ref).view(np.uint32)), tag
+
+
+def test_short_window_one_launch_capture_and_replay(dev):
+    """A short window's one-launch KQKV (a workgroup per (32-key split, head), the last workgroup of
+    a head merging through a per-head ticket) under graph capture: WKB (f32 W_kb) -> KQKV over a
+    256-key f16 cache at the 576 / 512 geometry, captured after an eager warm-up on a side stream
+    (which resolves the ticket array), then replayed three times with new q, cache and live length,
+    each replay run twice in a row (the tickets must be back at zero after every launch) and checked
+    bit for bit against the eager run and against the oracle at the f16-cache bar."""
+    Hs, DN, DK, DV, WS = 32, 128, 576, 512, 256
+    rng = np.random.default_rng(9600)
+    w_kb = (rng.standard_normal((Hs, DV, DN)) * 0.05).astype(np.float32)
+    scale = 1.0 / np.sqrt(192.0)
+    d_wkb = torch.from_numpy(w_kb).to(dev)
+    d_q = torch.zeros((1, Hs, DN + 64), dtype=torch.float32, device=dev)
+    d_kc = torch.zeros((WS, DK), dtype=torch.float16, device=dev)
+    d_mask = torch.full((1, WS), float("-inf"), dtype=torch.float32, device=dev)
+    d_qcur = torch.empty((1, Hs, DK), dtype=torch.float32, device=dev)
+    d_out = torch.empty((Hs, 1, DV), dtype=torch.float32, device=dev)
+    need = A.kqkv_workspace_bytes(d_kc, d_qcur, d_out)
+    assert need > 0                                           # the one-launch kernel's records
+    d_ws = torch.empty(need, dtype=torch.uint8, device=dev)
+
+    def step():
+        A.ggml_m4_wkb(d_wkb, d_q[:, :, :DN], out=d_qcur[:, :, :DV])
+        d_qcur[:, :, DV:].copy_(d_q[:, :, DN:])
+        A.ggml_m4_kqkv(d_kc, d_qcur, d_mask, scale, out=d_out, workspace=d_ws)
+
+    def load(seed):
+        r = np.random.default_rng(seed)
+        live = int(r.integers(40, WS + 1))
+        q = (r.standard_normal((1, Hs, DN + 64)) * 0.05).astype(np.float32)
+        kc = (r.standard_normal((WS, DK)) * 0.05).astype(np.float16)
+        m = np.full((1, WS), -np.inf, dtype=np.float32)
+        m[0, :live] = 0.0
+        d_q.copy_(torch.from_numpy(q))
+        d_kc.copy_(torch.from_numpy(kc))
+        d_mask.copy_(torch.from_numpy(m))
+        torch.cuda.synchronize()
+        return kc, m, live
+
+    load(1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, capture_error_mode="global"):
+        step()
+    torch.cuda.synchronize()
+
+    for rep, seed in enumerate((21, 22, 23)):
+        kc, m, live = load(seed)
+        step()
+        torch.cuda.synchronize()
+        eager = d_out.cpu().numpy()
+        qcur = d_qcur.cpu().numpy()
+        for k in range(2):
+            g.replay()
+            torch.cuda.synchronize()
+            got = d_out.cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), (rep, k)
+        ref = orc.kqkv(kc, qcur, m, scale, d_v=DV)
+        ea, er, rr = errs(got, ref)
+        say(f"one-launch replay {rep} (live {live}): vs oracle max_abs={ea:.3e} max_rel={er:.3e} rms_rel={rr:.3e}")
+        assert np.isfinite(got).all() and ea <= 1e-2 and er <= 3e-3, rep
