@@ -43,8 +43,9 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 COLD_BYTES = 512 << 20         # bytes one rotation of step inputs must exceed (2 x the MALL)
 GRAPH_MIN_STEPS = 64           # steps per captured graph, at least
 CAL_BYTES = 256 << 20          # calibration copy size (each way) for the HBM traffic counters
-TRAFFIC_FILES = {3: ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",      # per decode config
-                 4: ROOT / "profiles" / "kqkv_decode_f16_cfg4_traffic.json"}
+TRAFFIC_FILES = {(3, "f16"): ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",   # per (decode config, cache)
+                 (4, "f16"): ROOT / "profiles" / "kqkv_decode_f16_cfg4_traffic.json",
+                 (3, "q8"): ROOT / "profiles" / "kqkv_decode_q8_cfg3_traffic.json"}
 
 
 def partial_kernel_name(kc_f16: bool, n_kv: int, n_split: int, q8: bool = False) -> str:
@@ -569,7 +570,7 @@ def main() -> int:
     # HBM bytes per launch of the partial kernel, from the committed rocprofv3 counter summary
     # (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the calibration copy's factor)
     traffic = None
-    tf_path = TRAFFIC_FILES.get(args.config)
+    tf_path = TRAFFIC_FILES.get((args.config, args.cache))
     if tf_path is not None and tf_path.exists() and not args.batch:
         tr = json.loads(tf_path.read_text())
         if tr.get("config") == args.config and tr.get("splits") == S and tr.get("kernel") == roof["kernel"]:

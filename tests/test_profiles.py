@@ -9,17 +9,20 @@ import pytest
 import bench
 
 N_KV = {3: 32768, 4: 262144}
+KEY_BYTES = {"f16": 1152 + 4, "q8": 576 // 32 * 34 + 4}     # cache row + mask, per key
 
 
-@pytest.mark.parametrize("config", sorted(bench.TRAFFIC_FILES))
-def test_traffic_file_matches_its_config(config):
-    path = bench.TRAFFIC_FILES[config]
+@pytest.mark.parametrize("key", sorted(bench.TRAFFIC_FILES))
+def test_traffic_file_matches_its_config(key):
+    config, cache = key
+    path = bench.TRAFFIC_FILES[key]
     assert path.exists(), path
     tr = json.loads(path.read_text())
-    assert tr["config"] == config
+    assert tr["config"] == config and tr.get("cache", "f16") == cache
     import aubier_amd as A
-    assert tr["splits"] == A.default_splits(N_KV[config])     # the library's split count at this length
-    assert tr["alg_bytes"] == N_KV[config] * 1156 + 32 * 576 * 4
+    ctype = A.ops.TYPE_Q8_0 if cache == "q8" else A.ops.TYPE_F16
+    assert tr["splits"] == A.default_splits(N_KV[config], 32, ctype)    # the library's split count at this length
+    assert tr["alg_bytes"] == N_KV[config] * KEY_BYTES[cache] + 32 * 576 * 4
     cal = tr["calibration"]
     # a plain copy of B bytes each way reads about 2 B of FETCH_SIZE bytes per KiB counted and writes B
     assert cal["fetch_scale"] == pytest.approx(bench.CAL_BYTES / 1024 / cal["fetch_kib"], rel=1e-4)
@@ -32,7 +35,7 @@ def test_traffic_file_matches_its_config(config):
     assert tr["traffic_bytes"] == pytest.approx(fetch + write, rel=1e-4)
     # the cache is read once: reads within a few percent of the algorithmic bytes
     assert 0.98 < tr["fetch_bytes"] / tr["alg_bytes"] < 1.05
-    assert tr["kernel"] == bench.partial_kernel_name(True, N_KV[config], tr["splits"])
+    assert tr["kernel"] == bench.partial_kernel_name(True, N_KV[config], tr["splits"], q8=cache == "q8")
 
 
 def test_partial_kernel_name():
