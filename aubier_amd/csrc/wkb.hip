@@ -81,6 +81,11 @@ __global__ __launch_bounds__(256) void wkb_f32_kernel(WkbArgs a) {
 // results within a few f32 ulps of the f32 product.  A 16-d step of a wave whose largest operand
 // magnitude is 2^15 or more (hi would overflow f16) or below 2^-8 (its values would sit in f16's
 // subnormal range) runs on v_mfma_f32_32x32x2_f32 instead, on the same accumulator.
+// With two waves per SIMD the kernel is bound by the VALU work of the split, not by the MFMAs (32
+// values per lane per 16-d step against 12 MFMAs), so the split is written out instruction by
+// instruction: 3 VALU instructions per value with the range check (split_pair, v_max3_f32 on
+// absolute values), where the compiler's own f32 -> f16 -> f32 round trip and canonicalising max
+// took about 7.
 // A workgroup computes a 128-token x 128-column tile of one head, each wave a 64 x 64 quarter
 // (2 x 2 tiles of 32 x 32).  The operands pass through LDS in d-chunks of 32 (128 bytes of every
 // row): the chunk's q rows (A) and W rows (B) arrive by LDS DMA, 8 lanes fetching one row's whole
@@ -96,6 +101,32 @@ constexpr int WKB_GEMM_MIN_TOKENS = 16;
 constexpr int WG_T = 128;                   // tile rows (tokens) and columns
 constexpr int WG_DC = 32;                   // d per chunk
 constexpr int WG_STAGE = WG_T * WG_DC * 4;  // bytes of one operand in one stage (16 KB)
+
+// x = hi + 2^-11 lo for a pair of f32 values: hi = f16(x) (round to nearest even, v_cvt_pk_f16_f32),
+// d = x - hi exactly in f32 (v_fma_mix_f32 takes hi's f16 half as it is), lo = f16(2^11 d) rounded
+// once (v_fma_mixlo / mixhi_f16 write the low / high half): 2.5 VALU instructions per value.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t & hi, uint32_t & lo) {
+    uint32_t h, l;
+    float d0, d1;
+    const float two11 = 2048.0f;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(h) : "v"(x0), "v"(x1));
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d0) : "v"(h), "v"(x0));
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d1) : "v"(h), "v"(x1));
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(l) : "v"(d0), "s"(two11));
+    asm("v_fma_mixhi_f16 %0, %1, %2, 0" : "+v"(l) : "v"(d1), "s"(two11));
+    hi = h;
+    lo = l;
+}
+// the f16 pieces of 8 values (x0, then x1), in MFMA operand order
+__device__ __forceinline__ void split8(const f32x4 & x0, const f32x4 & x1, half8 & hi, half8 & lo) {
+    uint32_t h[4], l[4];
+    split_pair(x0[0], x0[1], h[0], l[0]);
+    split_pair(x0[2], x0[3], h[1], l[1]);
+    split_pair(x1[0], x1[1], h[2], l[2]);
+    split_pair(x1[2], x1[3], h[3], l[3]);
+    hi = __builtin_bit_cast(half8, u32x4{h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(half8, u32x4{l[0], l[1], l[2], l[3]});
+}
 
 struct WkbGemmLds {
     __attribute__((aligned(16))) char a[2][WG_STAGE];
@@ -183,33 +214,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     af[i][u] = *reinterpret_cast<const f32x4 *>(sa + aoff + apitch * 32 * i + slot);
                     bf[i][u] = *reinterpret_cast<const f32x4 *>(sb + boff + apitch * 32 * i + slot);
                 }
-            float mx = 0.0f;
+            // the largest magnitude among the wave's operands of this step: v_max3_f32 on absolute
+            // values, two per instruction (no canonicalisation of the loaded values), in two chains;
+            // the s_nop covers the VALU -> DPP read distance of the wave reduction
+            float mx = 0.0f, my = 0.0f;
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fmaxf(fabsf(af[i][u][e]), fabsf(bf[i][u][e])));
+                    for (int e = 0; e < 4; e += 2) {
+                        asm("v_max3_f32 %0, |%1|, |%2|, %0" : "+v"(mx) : "v"(af[i][u][e]), "v"(af[i][u][e + 1]));
+                        asm("v_max3_f32 %0, |%1|, |%2|, %0" : "+v"(my) : "v"(bf[i][u][e]), "v"(bf[i][u][e + 1]));
+                    }
+            asm("v_max_f32 %0, %0, %1\n\ts_nop 1" : "+v"(mx) : "v"(my));
             mx = wave_max(mx);
             if (mx < 32768.0f && (mx >= 0.00390625f || mx == 0.0f)) {
                 // x = hi + 2^-11 lo with hi = f16(x), lo = f16(2^11 (x - hi)) (x - hi exact in f32):
                 // 22 bits of x.  hi.hi on one accumulator, hi.lo + lo.hi on the other (lo.lo, below
                 // 2^-22 of the product, is dropped)
-                auto split = [](const f32x4 & x0, const f32x4 & x1, half8 & hi, half8 & lo) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float x = e < 4 ? x0[e] : x1[e - 4];
-                        const half_t h = (half_t)x;
-                        hi[e] = h;
-                        lo[e] = (half_t)((x - (float)h) * 2048.0f);
-                    }
-                };
                 half8 ah[2], al[2], bh[2], bl[2];
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    split(af[i][0], af[i][1], ah[i], al[i]);
-                    split(bf[i][0], bf[i][1], bh[i], bl[i]);
+                    split8(af[i][0], af[i][1], ah[i], al[i]);
+                    split8(bf[i][0], bf[i][1], bh[i], bl[i]);
                 }
+                // 3 wait states between the VALU writes above (inline asm, outside the compiler's
+                // hazard tracking) and the MFMAs that read them
+                asm volatile("s_nop 2" : "+v"(ah[0]), "+v"(ah[1]), "+v"(al[0]), "+v"(al[1]), "+v"(bh[0]), "+v"(bh[1]),
+                             "+v"(bl[0]), "+v"(bl[1]));
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
