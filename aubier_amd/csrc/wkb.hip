@@ -96,7 +96,10 @@ __global__ __launch_bounds__(256) void wkb_f32_kernel(WkbArgs a) {
 // is k-step e, in A and B alike: the k order inside an MFMA is free as long as both operands
 // agree).  Tiles are ordered so that the tiles of a head run on one XCD (workgroup i is dispatched
 // to XCD i mod 8), which keeps each head's q and W rows in one L2.  Two workgroups share a CU
-// (LDS-bound), so the kernel is held to 256 registers per lane.
+// (LDS-bound), so the kernel is held to 256 registers per lane.  The result leaves through the
+// ring once it is free: each wave's 64 x 64 quarter as rows in LDS, then 16-byte row chunks (16
+// stores of 1 KB per wave instead of 64 single-value stores, each with its own row address);
+// an output view whose rows are not 16-byte aligned takes the single-value stores.
 constexpr int WKB_GEMM_MIN_TOKENS = 16;
 constexpr int WG_T = 128;                   // tile rows (tokens) and columns
 constexpr int WG_DC = 32;                   // d per chunk
@@ -275,6 +278,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // t = t0 + 64 (w >> 1) + 32 i + 8 (r / 4) + 4 (lane >> 5) + (r & 3)
     char * db = reinterpret_cast<char *>(a.dst) + (size_t)h * a.d_nb1;
     const int tw = t0 + 64 * (w >> 1), cw = c0 + 64 * (w & 1);
+    const bool rows16 = ((reinterpret_cast<uintptr_t>(db) | (uintptr_t)a.d_nb2) & 15) == 0 && (a.d_v & 3) == 0;
+    if (rows16) {
+        // through LDS (the ring is free once every wave is past the last chunk): the wave's 64 x 64
+        // quarter as [64 rows][64 columns] in its own 16 KB, then out in 16-byte row chunks, four
+        // rows of 256 bytes per store instruction
+        __syncthreads();
+        float * qs = reinterpret_cast<float *>(&sh) + w * 64 * 64;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    qs[(32 * i + 8 * (r >> 2) + 4 * hh + (r & 3)) * 64 + 32 * j + r32] = acc[i][j][r];
+        const int ch = lane & 15, rq = lane >> 4;
+        const int col = cw + 4 * ch;
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int row = 4 * it + rq;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(qs + row * 64 + 4 * ch);
+            const int t = tw + row;
+            if (t < a.nt && col < a.d_v) *reinterpret_cast<f32x4 *>(db + (size_t)t * a.d_nb2 + 4 * col) = v;
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll

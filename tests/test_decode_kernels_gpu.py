@@ -228,6 +228,34 @@ def test_wkb_gemm_operand_range(dev, case):
     check(f"WKB GEMM {case} vs f64", got, ref64, 2e-6 * m, 2e-6)
 
 
+def test_wkb_gemm_output_views(dev):
+    """The many-token WKB GEMM writes 16-byte row chunks when the output rows are 16-byte aligned
+    and one value per lane otherwise.  Three outputs of one launch shape -- contiguous, the
+    engine's Qcur view ([nt, H, 576][..., :512]) and a view one float into a wider buffer (not
+    16-byte aligned) -- must agree bit for bit, match the oracle, and leave every value outside
+    the view as it was (partial 128-token tiles: nt = 130)."""
+    H, d_v, d_n, nt = 4, 512, 128, 130
+    g = np.random.default_rng(8820)
+    w = (g.standard_normal((H, d_v, d_n)) * 0.05).astype(np.float32)
+    q = (g.standard_normal((nt, H, d_n)) * 0.05).astype(np.float32)
+    ref = orc.wkb(w, q)
+    w_d, q_d = torch.from_numpy(w).to(dev), torch.from_numpy(q).to(dev)
+    outs = {}
+    outs["contiguous"] = A.ggml_m4_wkb(w_d, q_d)
+    qcur = torch.full((nt, H, 576), 7.0, dtype=torch.float32, device=dev)
+    outs["qcur_view"] = A.ggml_m4_wkb(w_d, q_d, out=qcur[:, :, :d_v])
+    wide = torch.full((nt, H, d_v + 4), 7.0, dtype=torch.float32, device=dev)
+    outs["unaligned_view"] = A.ggml_m4_wkb(w_d, q_d, out=wide[:, :, 1:1 + d_v])
+    torch.cuda.synchronize()
+    base = outs["contiguous"].cpu().numpy()
+    check("WKB GEMM contiguous vs oracle", base, ref, 1e-3, 1e-5)
+    for name in ("qcur_view", "unaligned_view"):
+        got = outs[name].cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), name
+    assert (qcur[:, :, d_v:] == 7.0).all().item()
+    assert (wide[:, :, 0] == 7.0).all().item() and (wide[:, :, 1 + d_v:] == 7.0).all().item()
+
+
 @pytest.mark.parametrize("d_n,d_v", [(128, 512), (64, 256)])
 @pytest.mark.parametrize("nt", [1, 5, 16, 37, 130])
 def test_wkb_token_counts(dev, d_n, d_v, nt):
