@@ -45,7 +45,9 @@ GRAPH_MIN_STEPS = 64           # steps per captured graph, at least
 CAL_BYTES = 256 << 20          # calibration copy size (each way) for the HBM traffic counters
 TRAFFIC_FILES = {(3, "f16"): ROOT / "profiles" / "kqkv_decode_f16_cfg3_traffic.json",   # per (decode config, cache)
                  (4, "f16"): ROOT / "profiles" / "kqkv_decode_f16_cfg4_traffic.json",
-                 (3, "q8"): ROOT / "profiles" / "kqkv_decode_q8_cfg3_traffic.json"}
+                 (3, "q8"): ROOT / "profiles" / "kqkv_decode_q8_cfg3_traffic.json",
+                 (4, "q8"): ROOT / "profiles" / "kqkv_decode_q8_cfg4_traffic.json",
+                 (2, "f16"): ROOT / "profiles" / "kqkv_decode_f16_cfg2_traffic.json"}
 
 
 def partial_kernel_name(kc_f16: bool, n_kv: int, n_split: int, q8: bool = False) -> str:

@@ -8,7 +8,7 @@ import pytest
 
 import bench
 
-N_KV = {3: 32768, 4: 262144}
+N_KV = {2: 4096, 3: 32768, 4: 262144}
 KEY_BYTES = {"f16": 1152 + 4, "q8": 576 // 32 * 34 + 4}     # cache row + mask, per key
 
 
@@ -33,8 +33,9 @@ def test_traffic_file_matches_its_config(key):
     assert tr["fetch_bytes"] == pytest.approx(fetch, rel=1e-4)
     assert tr["write_bytes"] == pytest.approx(write, rel=1e-4)
     assert tr["traffic_bytes"] == pytest.approx(fetch + write, rel=1e-4)
-    # the cache is read once: reads within a few percent of the algorithmic bytes
-    assert 0.98 < tr["fetch_bytes"] / tr["alg_bytes"] < 1.05
+    # the cache is read once: reads within a few percent of the algorithmic bytes, plus at most one
+    # fetch of the 73,728-byte Qcur block per XCD L2 (8), which weighs only at short windows
+    assert 0.98 * tr["alg_bytes"] < tr["fetch_bytes"] < 1.05 * tr["alg_bytes"] + 8 * 32 * 576 * 4
     assert tr["kernel"] == bench.partial_kernel_name(True, N_KV[config], tr["splits"], q8=cache == "q8")
 
 
